@@ -1,0 +1,424 @@
+// C ABI of libmans_hip.so: context, corpus handles, stream/workspace pool,
+// error channel and the proof loop of the exact flat scan.
+//
+// The pool stands in for CommandQueuePool (CommandQueuePool.swift:27-31) and
+// FlatWorkspacePool (FlatGPUSearch.swift:1070-1139): every call borrows one
+// HIP stream plus its device workspace and returns them when done, so a
+// context serves concurrent callers.  Streams use the default priority.
+#include "mans_hip.h"
+#include "mans_internal.hpp"
+#include "mans_runtime.hpp"
+
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+using namespace mans;
+
+namespace mans {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    std::string msg = std::string(what) + ": " + hipGetErrorString(e);
+    if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation)
+        return fail(MANS_RESOURCE_EXHAUSTED, msg);
+    return fail(MANS_EXECUTION_FAILED, msg);
+}
+
+hipError_t DevBuf::ensure(size_t need, bool inject_fail) {
+    if (need <= bytes && p) return hipSuccess;
+    if (inject_fail) return hipErrorOutOfMemory;
+    if (p) {
+        hipError_t e = hipFree(p);
+        if (e != hipSuccess) return e;
+        p = nullptr;
+        bytes = 0;
+    }
+    size_t alloc = need < 256 ? 256 : need;
+    hipError_t e = hipMalloc(&p, alloc);
+    if (e != hipSuccess) {
+        p = nullptr;
+        return e;
+    }
+    bytes = alloc;
+    return hipSuccess;
+}
+
+void DevBuf::release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    bytes = 0;
+}
+
+hipError_t PinnedBuf::ensure(size_t need) {
+    if (need <= bytes && p) return hipSuccess;
+    if (p) (void)hipHostFree(p);
+    p = nullptr;
+    bytes = 0;
+    size_t alloc = need < 256 ? 256 : need;
+    hipError_t e = hipHostMalloc(&p, alloc, hipHostMallocDefault);
+    if (e != hipSuccess) {
+        p = nullptr;
+        return e;
+    }
+    bytes = alloc;
+    return hipSuccess;
+}
+
+void PinnedBuf::release() {
+    if (p) (void)hipHostFree(p);
+    p = nullptr;
+    bytes = 0;
+}
+
+Slot::~Slot() {
+    for (DevBuf* b : {&queries, &qidx, &cand, &dist, &ids, &status, &aux0, &aux1, &aux2, &aux3})
+        b->release();
+    status_h.release();
+    if (ev0) (void)hipEventDestroy(ev0);
+    if (ev1) (void)hipEventDestroy(ev1);
+    if (stream) (void)hipStreamDestroy(stream);
+}
+
+}  // namespace mans
+
+Slot* mans_ctx::acquire() {
+    {
+        std::lock_guard<std::mutex> g(mu);
+        if (!free_slots.empty()) {
+            Slot* s = free_slots.back();
+            free_slots.pop_back();
+            return s;
+        }
+    }
+    Slot* s = new Slot();
+    if (hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreate(&s->ev0) != hipSuccess || hipEventCreate(&s->ev1) != hipSuccess) {
+        delete s;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> g(mu);
+    all_slots.push_back(s);
+    return s;
+}
+
+void mans_ctx::release(Slot* s) {
+    std::lock_guard<std::mutex> g(mu);
+    free_slots.push_back(s);
+}
+
+void mans_ctx::time_begin(Slot* s, hipStream_t st) {
+    if (timing) (void)hipEventRecord(s->ev0, st);
+}
+
+void mans_ctx::time_end(Slot* s, hipStream_t st, const char* name) {
+    if (!timing) return;
+    (void)hipEventRecord(s->ev1, st);
+    if (hipEventSynchronize(s->ev1) != hipSuccess) return;
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, s->ev0, s->ev1) != hipSuccess) return;
+    std::lock_guard<std::mutex> g(tmu);
+    auto& t = times[name];
+    t.first += ms;
+    t.second += 1;
+}
+
+extern "C" {
+
+const char* mans_last_error(void) { return g_last_error.c_str(); }
+
+int mans_ctx_create(int device, mans_ctx** out) {
+    if (!out) return fail(MANS_SEARCH_FAILED, "mans_ctx_create: out is NULL");
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0)
+        return fail(MANS_DEVICE_NOT_SUPPORTED, "no HIP device present");
+    if (device < 0 || device >= count)
+        return fail(MANS_DEVICE_NOT_SUPPORTED, "device index out of range");
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess)
+        return fail(MANS_DEVICE_NOT_SUPPORTED, "hipGetDeviceProperties failed");
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(MANS_DEVICE_NOT_SUPPORTED,
+                    std::string("device is ") + prop.gcnArchName + ", this library is built for gfx950");
+    mans_ctx* c = new mans_ctx();
+    c->device = device;
+    c->num_cus = prop.multiProcessorCount;
+    const char* f = std::getenv("MANS_HIP_FAIL");
+    if (f) {
+        c->fail_alloc = std::strstr(f, "alloc") != nullptr;
+        c->fail_launch = std::strstr(f, "launch") != nullptr;
+    }
+    DeviceGuard dg(device);
+    if (hipFree(nullptr) != hipSuccess) {
+        delete c;
+        return fail(MANS_DEVICE_NOT_SUPPORTED, "HIP runtime initialisation failed");
+    }
+    *out = c;
+    return MANS_OK;
+}
+
+void mans_ctx_destroy(mans_ctx* ctx) {
+    if (!ctx) return;
+    {
+        DeviceGuard dg(ctx->device);
+        for (Slot* s : ctx->all_slots) {
+            if (s->stream) (void)hipStreamSynchronize(s->stream);
+            delete s;
+        }
+    }
+    delete ctx;
+}
+
+int mans_corpus_upload_f32(mans_ctx* ctx, const float* rows, int64_t n, int64_t dim,
+                           mans_corpus** out) {
+    if (!ctx || !out) return fail(MANS_SEARCH_FAILED, "mans_corpus_upload_f32: NULL argument");
+    *out = nullptr;
+    if (n < 0 || dim <= 0 || (n > 0 && !rows))
+        return fail(MANS_DIMENSION_MISMATCH, "mans_corpus_upload_f32: bad shape");
+    if (dim > 8192)
+        return fail(MANS_SEARCH_FAILED, "mans_corpus_upload_f32: dim above 8192 is not supported");
+    if (n > (int64_t)0xFFFFFFFEll)
+        return fail(MANS_SEARCH_FAILED, "corpus larger than the 32-bit id space");
+    DeviceGuard dg(ctx->device);
+    mans_corpus* c = new mans_corpus();
+    c->ctx = ctx;
+    c->n = n;
+    c->dim = dim;
+    size_t bytes = (size_t)n * (size_t)dim * sizeof(float);
+    hipError_t e = c->rows.ensure(bytes ? bytes : 4, ctx->fail_alloc);
+    if (e == hipSuccess) e = c->norms.ensure((size_t)(n ? n : 1) * sizeof(float), ctx->fail_alloc);
+    if (e != hipSuccess) {
+        delete c;
+        return hip_fail(e, "corpus allocation");
+    }
+    if (n > 0) {
+        e = hipMemcpy(c->rows.p, rows, bytes, hipMemcpyHostToDevice);
+        if (e == hipSuccess)
+            e = launch_row_norms((const float*)c->rows.p, n, (int)dim, (float*)c->norms.p, nullptr);
+        if (e == hipSuccess) e = hipDeviceSynchronize();
+    }
+    if (e != hipSuccess) {
+        delete c;
+        return hip_fail(e, "corpus upload");
+    }
+    *out = c;
+    return MANS_OK;
+}
+
+int mans_corpus_write_rows(mans_corpus* c, int64_t first_row, const float* rows, int64_t count) {
+    if (!c || (count > 0 && !rows)) return fail(MANS_SEARCH_FAILED, "mans_corpus_write_rows: NULL");
+    if (first_row < 0 || count < 0 || first_row + count > c->n)
+        return fail(MANS_SEARCH_FAILED, "mans_corpus_write_rows: row range outside the corpus");
+    if (count == 0) return MANS_OK;
+    DeviceGuard dg(c->ctx->device);
+    std::lock_guard<std::mutex> g(c->mu);
+    float* dst = (float*)c->rows.p + first_row * c->dim;
+    hipError_t e = hipMemcpy(dst, rows, (size_t)count * c->dim * sizeof(float), hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = launch_row_norms(dst, count, (int)c->dim, (float*)c->norms.p + first_row, nullptr);
+    if (e == hipSuccess && c->int8_valid)
+        e = int8_refresh_rows(c, first_row, count, nullptr);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) return hip_fail(e, "corpus write");
+    return MANS_OK;
+}
+
+int mans_corpus_invalidate(mans_corpus* c) {
+    if (!c) return fail(MANS_SEARCH_FAILED, "mans_corpus_invalidate: NULL");
+    std::lock_guard<std::mutex> g(c->mu);
+    c->int8_valid = false;
+    return MANS_OK;
+}
+
+void mans_corpus_release(mans_corpus* c) {
+    if (!c) return;
+    DeviceGuard dg(c->ctx->device);
+    (void)hipDeviceSynchronize();
+    delete c;
+}
+
+int64_t mans_corpus_count(const mans_corpus* c) { return c ? c->n : -1; }
+int64_t mans_corpus_dim(const mans_corpus* c) { return c ? c->dim : -1; }
+
+int mans_timing_enable(mans_ctx* ctx, int enable) {
+    if (!ctx) return fail(MANS_SEARCH_FAILED, "NULL context");
+    ctx->timing = enable != 0;
+    return MANS_OK;
+}
+
+int mans_timing_read(mans_ctx* ctx, const char* kernel, double* total_ms, int64_t* launches) {
+    if (!ctx || !kernel) return fail(MANS_SEARCH_FAILED, "NULL argument");
+    std::lock_guard<std::mutex> g(ctx->tmu);
+    auto it = ctx->times.find(kernel);
+    if (total_ms) *total_ms = it == ctx->times.end() ? 0.0 : it->second.first;
+    if (launches) *launches = it == ctx->times.end() ? 0 : it->second.second;
+    return MANS_OK;
+}
+
+int mans_timing_reset(mans_ctx* ctx) {
+    if (!ctx) return fail(MANS_SEARCH_FAILED, "NULL context");
+    std::lock_guard<std::mutex> g(ctx->tmu);
+    ctx->times.clear();
+    return MANS_OK;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Exact flat scan driver.
+// ---------------------------------------------------------------------------
+
+namespace mans {
+
+static int pow2_ceil(int64_t x) {
+    int p = 1;
+    while (p < x) p <<= 1;
+    return p;
+}
+
+hipError_t fill_empty(float* dist, uint32_t* ids, int64_t count, hipStream_t s) {
+    if (count <= 0) return hipSuccess;
+    hipError_t e = hipMemsetD32Async((hipDeviceptr_t)dist, 0x7F7FFFFF, (size_t)count, s);
+    if (e == hipSuccess) e = hipMemsetD32Async((hipDeviceptr_t)ids, 0xFFFFFFFF, (size_t)count, s);
+    return e;
+}
+
+// Runs the flat scan for queries already in device memory.  The proof loop
+// (kc x4 per round, exact keys past kc = 1024) mirrors the budget growth of
+// BoundedExactScan.swift:96-121.
+static int flat_search_chunk(mans_ctx* ctx, const mans_corpus* c, const float* d_q, int64_t nq,
+                             int64_t k, uint32_t metric, float* d_dist, uint32_t* d_ids,
+                             hipStream_t st, Slot* slot);
+
+// Queries go through in chunks so the grid's y extent and the candidate
+// workspace stay bounded.
+int flat_search_run(mans_ctx* ctx, const mans_corpus* c, const float* d_q, int64_t nq, int64_t k,
+                    uint32_t metric, float* d_dist, uint32_t* d_ids, hipStream_t st, Slot* slot) {
+    if (metric > 2) return fail(MANS_SEARCH_FAILED, "flat scan does not support this metric");
+    if (nq <= 0 || k <= 0) return MANS_OK;
+    if (ctx->fail_launch) return fail(MANS_EXECUTION_FAILED, "injected launch failure");
+    const int64_t chunk = 16384;
+    for (int64_t q0 = 0; q0 < nq; q0 += chunk) {
+        int64_t m = std::min(chunk, nq - q0);
+        int rc = flat_search_chunk(ctx, c, d_q + q0 * c->dim, m, k, metric, d_dist + q0 * k,
+                                   d_ids + q0 * k, st, slot);
+        if (rc != MANS_OK) return rc;
+    }
+    return MANS_OK;
+}
+
+static int flat_search_chunk(mans_ctx* ctx, const mans_corpus* c, const float* d_q, int64_t nq,
+                             int64_t k, uint32_t metric, float* d_dist, uint32_t* d_ids,
+                             hipStream_t st, Slot* slot) {
+    const int64_t n = c->n;
+    const int dim = (int)c->dim;
+    const int kstride = (int)k;
+    if (n == 0) {
+        hipError_t e = fill_empty(d_dist, d_ids, nq * k, st);
+        if (e == hipSuccess) e = hipStreamSynchronize(st);
+        return e == hipSuccess ? MANS_OK : hip_fail(e, "fill");
+    }
+    const int keff = (int)std::min<int64_t>(std::min<int64_t>(k, MANS_MAX_TOP_K), n);
+    int kc = pow2_ceil(std::max(32, 2 * keff));
+    // The float4 path needs 16-byte aligned rows and queries.
+    bool exact = flat_nch_for_dim(dim) == 0 || (reinterpret_cast<uintptr_t>(d_q) & 15u) != 0;
+    std::vector<uint32_t> pending;  // empty = all queries
+    int64_t npend = nq;
+    for (;;) {
+        if (exact) kc = pow2_ceil(std::max(32, keff));
+        FlatPlan p = plan_flat(n, npend, kc);
+        const uint32_t* d_qidx = nullptr;
+        hipError_t e = hipSuccess;
+        if (!pending.empty()) {
+            e = slot->qidx.ensure(pending.size() * sizeof(uint32_t), ctx->fail_alloc);
+            if (e == hipSuccess)
+                e = hipMemcpyAsync(slot->qidx.p, pending.data(), pending.size() * sizeof(uint32_t),
+                                   hipMemcpyHostToDevice, st);
+            d_qidx = (const uint32_t*)slot->qidx.p;
+        }
+        if (e == hipSuccess)
+            e = slot->cand.ensure((size_t)npend * p.nblk * p.kc * sizeof(uint64_t), ctx->fail_alloc);
+        if (e == hipSuccess) e = slot->status.ensure((size_t)npend, ctx->fail_alloc);
+        if (e == hipSuccess) e = slot->status_h.ensure((size_t)npend);
+        if (e != hipSuccess) return hip_fail(e, "flat scan workspace");
+        ctx->time_begin(slot, st);
+        e = launch_flat_scan(p, exact, (const float*)c->rows.p, (const float*)c->norms.p, n, dim,
+                             d_q, d_qidx, npend, (int)metric, (uint64_t*)slot->cand.p, st);
+        ctx->time_end(slot, st, "flat_scan");
+        if (e == hipSuccess)
+            e = launch_flat_merge(p, (const float*)c->rows.p, (const float*)c->norms.p, n, dim, d_q,
+                                  d_qidx, npend, (int)metric, keff, kstride,
+                                  (const uint64_t*)slot->cand.p, d_dist, d_ids,
+                                  (uint8_t*)slot->status.p, st);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(slot->status_h.p, slot->status.p, (size_t)npend,
+                               hipMemcpyDeviceToHost, st);
+        if (e == hipSuccess) e = hipStreamSynchronize(st);
+        if (e != hipSuccess) return hip_fail(e, "flat scan");
+        const uint8_t* sh = (const uint8_t*)slot->status_h.p;
+        std::vector<uint32_t> next;
+        for (int64_t i = 0; i < npend; ++i)
+            if (sh[i]) next.push_back(pending.empty() ? (uint32_t)i : pending[i]);
+        if (next.empty()) return MANS_OK;
+        if (exact) return fail(MANS_SEARCH_FAILED, "exact round failed its own proof");
+        pending.swap(next);
+        npend = (int64_t)pending.size();
+        kc *= 4;
+        if (kc > 1024) exact = true;
+        ctx->proof_retries += npend;
+    }
+}
+
+}  // namespace mans
+
+extern "C" {
+
+int mans_flat_search_device(mans_ctx* ctx, const mans_corpus* c, const float* d_queries,
+                            int64_t nq, int64_t k, uint32_t metric, float* d_out_dist,
+                            uint32_t* d_out_ids, void* stream) {
+    if (!ctx || !c) return fail(MANS_SEARCH_FAILED, "NULL context or corpus");
+    if (nq > 0 && k > 0 && (!d_queries || !d_out_dist || !d_out_ids))
+        return fail(MANS_SEARCH_FAILED, "NULL buffer");
+    DeviceGuard dg(ctx->device);
+    SlotLease lease(ctx);
+    if (!lease.slot) return fail(MANS_RESOURCE_EXHAUSTED, "could not create a HIP stream");
+    hipStream_t st = stream ? (hipStream_t)stream : lease.slot->stream;
+    return flat_search_run(ctx, c, d_queries, nq, k, metric, d_out_dist, d_out_ids, st, lease.slot);
+}
+
+int mans_flat_search(mans_ctx* ctx, const mans_corpus* c, const float* queries, int64_t nq,
+                     int64_t k, uint32_t metric, float* out_dist, uint32_t* out_ids) {
+    if (!ctx || !c) return fail(MANS_SEARCH_FAILED, "NULL context or corpus");
+    if (nq <= 0 || k <= 0) return MANS_OK;
+    if (!queries || !out_dist || !out_ids) return fail(MANS_SEARCH_FAILED, "NULL buffer");
+    DeviceGuard dg(ctx->device);
+    SlotLease lease(ctx);
+    Slot* s = lease.slot;
+    if (!s) return fail(MANS_RESOURCE_EXHAUSTED, "could not create a HIP stream");
+    size_t qbytes = (size_t)nq * c->dim * sizeof(float);
+    size_t obytes = (size_t)nq * k * sizeof(float);
+    hipError_t e = s->queries.ensure(qbytes, ctx->fail_alloc);
+    if (e == hipSuccess) e = s->dist.ensure(obytes, ctx->fail_alloc);
+    if (e == hipSuccess) e = s->ids.ensure(obytes, ctx->fail_alloc);
+    if (e == hipSuccess) e = hipMemcpyAsync(s->queries.p, queries, qbytes, hipMemcpyHostToDevice, s->stream);
+    if (e != hipSuccess) return hip_fail(e, "flat scan staging");
+    int rc = flat_search_run(ctx, c, (const float*)s->queries.p, nq, k, metric, (float*)s->dist.p,
+                             (uint32_t*)s->ids.p, s->stream, s);
+    if (rc != MANS_OK) return rc;
+    e = hipMemcpyAsync(out_dist, s->dist.p, obytes, hipMemcpyDeviceToHost, s->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(out_ids, s->ids.p, obytes, hipMemcpyDeviceToHost, s->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+    if (e != hipSuccess) return hip_fail(e, "flat scan results");
+    return MANS_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,193 @@
+// Device-side building blocks shared by the scan kernels (gfx950, wave64).
+//
+// All HIP sources are compiled with -ffp-contract=off: a multiply and an add
+// written separately stay two correctly rounded operations, which is what
+// the reference's scalar dots.c loop (dots.c:40-47) executes on x86-64.
+// Fast paths that may fuse say so with an explicit fmaf().
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mans {
+
+constexpr uint32_t kEmptyId = 0xFFFFFFFFu;
+constexpr uint64_t kEmptySlot = ~0ull;
+constexpr int kMetricCosine = 0;
+constexpr int kMetricL2 = 1;
+constexpr int kMetricIP = 2;
+constexpr float kFltMax = 3.402823466e+38f;
+
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+// 128-bit streaming load (the corpus is read once per query batch).
+__device__ __forceinline__ f4v load_stream(const float* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const f4v*>(p));
+}
+
+// Intra-wave barrier for LDS traffic between lanes of one wave.
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Order-preserving map float -> uint32 (-0 is folded onto +0 first, so the
+// packed order agrees with float comparison).
+__device__ __forceinline__ uint32_t ordered_bits(float x) {
+    x = x + 0.0f;
+    uint32_t u = __float_as_uint(x);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float from_ordered_bits(uint32_t o) {
+    uint32_t u = (o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o;
+    return __uint_as_float(u);
+}
+
+// (key, id) packed so that unsigned comparison is (key asc, id asc).
+__device__ __forceinline__ uint64_t pack_slot(float key, uint32_t id) {
+    return ((uint64_t)ordered_bits(key) << 32) | (uint64_t)id;
+}
+__device__ __forceinline__ float slot_key(uint64_t s) { return from_ordered_bits((uint32_t)(s >> 32)); }
+__device__ __forceinline__ uint32_t slot_id(uint64_t s) { return (uint32_t)s; }
+
+// Host distance formulas (ParallelFlatScan.swift:237-257, BoundedExactScan.swift:346-363,
+// IVFFlatSearch.swift:294-311), evaluated with the same correctly rounded
+// operations in the same order.
+__device__ __forceinline__ float host_distance(float dot, float qn, float vn, int metric) {
+    if (metric == kMetricIP) return -dot;
+    if (metric == kMetricL2) {
+        float d = qn - 2.0f * dot + vn;
+        return d > 0.0f ? d : 0.0f;
+    }
+    float denom = sqrtf(qn * vn);
+    return denom < 1e-10f ? 1.0f : 1.0f - dot / denom;
+}
+
+// Sequential dot in the order of dots.c:40-47.
+__device__ __forceinline__ float exact_dot(const float* __restrict__ a, const float* __restrict__ b,
+                                           int dim) {
+    float acc = 0.0f;
+    for (int d = 0; d < dim; ++d) acc = acc + a[d] * b[d];
+    return acc;
+}
+
+// Sum over the 16 lanes of a DPP row; every lane of the row gets the total.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));  // row_ror:8
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false));  // row_ror:4
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+    return v;
+}
+
+__device__ __forceinline__ uint64_t lanemask_lt() {
+    uint32_t lane = __lane_id();
+    return lane == 0 ? 0ull : (~0ull >> (64 - lane));
+}
+
+// Ascending bitonic sort of `size` (power of two) packed slots in LDS by one wave.
+__device__ inline void wave_bitonic_sort(uint64_t* buf, int size) {
+    const int lane = __lane_id();
+    for (int k2 = 2; k2 <= size; k2 <<= 1) {
+        for (int j = k2 >> 1; j > 0; j >>= 1) {
+            for (int i = lane; i < size; i += 64) {
+                int ixj = i ^ j;
+                if (ixj > i) {
+                    uint64_t a = buf[i], b = buf[ixj];
+                    bool up = (i & k2) == 0;
+                    if ((a > b) == up) {
+                        buf[i] = b;
+                        buf[ixj] = a;
+                    }
+                }
+            }
+            wave_sync();
+        }
+    }
+}
+
+// Ascending bitonic sort of `size` (power of two) slots in LDS by the whole block.
+__device__ inline void block_bitonic_sort(uint64_t* buf, int size) {
+    const int tid = threadIdx.x, nt = blockDim.x;
+    for (int k2 = 2; k2 <= size; k2 <<= 1) {
+        for (int j = k2 >> 1; j > 0; j >>= 1) {
+            for (int i = tid; i < size; i += nt) {
+                int ixj = i ^ j;
+                if (ixj > i) {
+                    uint64_t a = buf[i], b = buf[ixj];
+                    bool up = (i & k2) == 0;
+                    if ((a > b) == up) {
+                        buf[i] = b;
+                        buf[ixj] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// Wave-private top-`kc` selector over a stream of (key, id) offers.
+// Offers with key <= threshold are appended to an LDS buffer of `cap` slots
+// (cap a power of two, cap >= kc + 64); when the buffer cannot take another
+// full wave of offers it is sorted and cut back to kc, and the threshold
+// becomes the kc-th key.  Every slot it drops has key >= the final kc-th
+// key, which is what the lower-bound proofs downstream rely on.
+struct WaveTopK {
+    uint64_t* buf;
+    int cap;
+    int kc;
+    int count;
+    float thresh;
+
+    __device__ void init(uint64_t* b, int capacity, int keep) {
+        buf = b;
+        cap = capacity;
+        kc = keep;
+        count = 0;
+        thresh = __int_as_float(0x7F800000);  // +inf
+    }
+
+    __device__ void compact() {
+        const int lane = __lane_id();
+        for (int i = count + lane; i < cap; i += 64) buf[i] = kEmptySlot;
+        wave_sync();
+        wave_bitonic_sort(buf, cap);
+        if (count >= kc) {
+            count = kc;
+            thresh = slot_key(buf[kc - 1]);
+        }
+    }
+
+    __device__ __forceinline__ void offer(bool valid, float key, uint32_t id) {
+        bool pass = valid && key <= thresh;
+        uint64_t mask = __ballot(pass);
+        if (mask == 0) return;
+        if (pass) {
+            int pos = count + __popcll(mask & lanemask_lt());
+            buf[pos] = pack_slot(key, id);
+        }
+        count += __popcll(mask);
+        if (count > cap - 64) {
+            wave_sync();
+            compact();
+        }
+    }
+
+    // Sorts the buffer; slots [0, min(count, kc)) hold the result, the rest
+    // of [0, cap) is padded with kEmptySlot.
+    __device__ void finish() {
+        wave_sync();
+        const int lane = __lane_id();
+        for (int i = count + lane; i < cap; i += 64) buf[i] = kEmptySlot;
+        wave_sync();
+        wave_bitonic_sort(buf, cap);
+        if (count > kc) count = kc;
+        for (int i = count + lane; i < cap; i += 64) buf[i] = kEmptySlot;
+        wave_sync();
+    }
+};
+
+}  // namespace mans

@@ -1,0 +1,47 @@
+// Entry points whose kernels are not in this build yet.  Each reports
+// MANS_PIPELINE_UNAVAILABLE (tier-degradeable, Errors.swift:21-31), so a
+// caller falls back to the next tier instead of failing.
+#include "mans_hip.h"
+#include "mans_runtime.hpp"
+
+using namespace mans;
+
+namespace mans {
+hipError_t int8_refresh_rows(mans_corpus*, int64_t, int64_t, hipStream_t) { return hipSuccess; }
+}
+
+static int unavailable(const char* what) {
+    return fail(MANS_PIPELINE_UNAVAILABLE, std::string(what) + " is not available in this build");
+}
+
+extern "C" {
+int mans_int8_search(mans_ctx*, mans_corpus*, const float*, int64_t, int64_t, uint32_t, int32_t,
+                     int64_t, float*, uint32_t*, int32_t*) { return unavailable("int8 scan"); }
+int mans_int8_search_device(mans_ctx*, mans_corpus*, const float*, int64_t, int64_t, uint32_t,
+                            int32_t, int64_t, float*, uint32_t*, void*) { return unavailable("int8 scan"); }
+int mans_int8_codes_download(mans_ctx*, mans_corpus*, int8_t*, float*, float*, float*, float*) {
+    return unavailable("int8 codes");
+}
+int mans_ivf_flat_build(mans_ctx*, const mans_corpus*, const float*, int64_t, uint32_t, mans_ivf** out) {
+    if (out) *out = nullptr;
+    return unavailable("IVF-flat");
+}
+int mans_kmeans(mans_ctx*, const mans_corpus*, int64_t, int64_t, uint32_t, float*) { return unavailable("k-means"); }
+int mans_ivf_flat_search(mans_ctx*, const mans_ivf*, const float*, int64_t, int64_t, int64_t, float*,
+                         uint32_t*, int32_t*) { return unavailable("IVF-flat"); }
+int mans_ivf_flat_search_device(mans_ctx*, const mans_ivf*, const float*, int64_t, int64_t, int64_t,
+                                float*, uint32_t*, void*) { return unavailable("IVF-flat"); }
+int mans_ivf_download_lists(const mans_ivf*, int64_t*, uint32_t*) { return unavailable("IVF-flat"); }
+void mans_ivf_release(mans_ivf*) {}
+int mans_ivfpq_build(mans_ctx*, const mans_corpus*, const float*, int64_t, const float*, int64_t,
+                     uint32_t, mans_ivfpq** out) {
+    if (out) *out = nullptr;
+    return unavailable("IVF-PQ");
+}
+int mans_ivfpq_search(mans_ctx*, const mans_ivfpq*, const float*, int64_t, int64_t, int64_t, int64_t,
+                      float*, uint32_t*) { return unavailable("IVF-PQ"); }
+int mans_ivfpq_search_device(mans_ctx*, const mans_ivfpq*, const float*, int64_t, int64_t, int64_t,
+                             int64_t, float*, uint32_t*, void*) { return unavailable("IVF-PQ"); }
+int mans_ivfpq_download_codes(const mans_ivfpq*, uint8_t*, int32_t*) { return unavailable("IVF-PQ"); }
+void mans_ivfpq_release(mans_ivfpq*) {}
+}

@@ -1,0 +1,106 @@
+// Host-side runtime objects behind the C ABI handles.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <atomic>
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "mans_hip.h"
+
+namespace mans {
+
+int fail(int code, const std::string& msg);
+int hip_fail(hipError_t e, const char* what);
+
+struct DevBuf {
+    void* p = nullptr;
+    size_t bytes = 0;
+    hipError_t ensure(size_t need, bool inject_fail);
+    void release();
+    ~DevBuf() { release(); }
+};
+
+struct PinnedBuf {
+    void* p = nullptr;
+    size_t bytes = 0;
+    hipError_t ensure(size_t need);
+    void release();
+    ~PinnedBuf() { release(); }
+};
+
+// One pooled stream with its workspace.
+struct Slot {
+    hipStream_t stream = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    DevBuf queries, qidx, cand, dist, ids, status;
+    DevBuf aux0, aux1, aux2, aux3;
+    PinnedBuf status_h;
+    ~Slot();
+};
+
+struct DeviceGuard {
+    int prev = -1;
+    explicit DeviceGuard(int d) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        (void)hipSetDevice(d);
+    }
+    ~DeviceGuard() {
+        if (prev >= 0) (void)hipSetDevice(prev);
+    }
+};
+
+}  // namespace mans
+
+struct mans_ctx {
+    int device = 0;
+    int num_cus = 256;
+    bool fail_alloc = false;   // MANS_HIP_FAIL=alloc: every workspace allocation fails
+    bool fail_launch = false;  // MANS_HIP_FAIL=launch: every search reports a failed launch
+    std::mutex mu;
+    std::vector<mans::Slot*> free_slots;
+    std::vector<mans::Slot*> all_slots;
+    std::atomic<bool> timing{false};
+    std::atomic<int64_t> proof_retries{0};
+    std::mutex tmu;
+    std::map<std::string, std::pair<double, int64_t>> times;
+
+    mans::Slot* acquire();
+    void release(mans::Slot* s);
+    void time_begin(mans::Slot* s, hipStream_t st);
+    void time_end(mans::Slot* s, hipStream_t st, const char* name);
+};
+
+struct mans_corpus {
+    mans_ctx* ctx = nullptr;
+    int64_t n = 0;
+    int64_t dim = 0;
+    mans::DevBuf rows;   // n x dim f32, row-major
+    mans::DevBuf norms;  // n f32, squared norms in the dots.c order
+    std::mutex mu;
+    // int8 planes (Int8CodeCache.swift:22-108), built on first use.
+    bool int8_valid = false;
+    mans::DevBuf i8_codes, i8_u, i8_w, i8_normsq, i8_invsqrt;
+};
+
+namespace mans {
+
+struct SlotLease {
+    mans_ctx* ctx;
+    Slot* slot;
+    explicit SlotLease(mans_ctx* c) : ctx(c), slot(c->acquire()) {}
+    ~SlotLease() {
+        if (slot) ctx->release(slot);
+    }
+};
+
+hipError_t fill_empty(float* dist, uint32_t* ids, int64_t count, hipStream_t s);
+int flat_search_run(mans_ctx* ctx, const mans_corpus* c, const float* d_q, int64_t nq, int64_t k,
+                    uint32_t metric, float* d_dist, uint32_t* d_ids, hipStream_t st, Slot* slot);
+hipError_t int8_refresh_rows(mans_corpus* c, int64_t first_row, int64_t count, hipStream_t s);
+
+}  // namespace mans
