@@ -80,9 +80,12 @@ void PinnedBuf::release() {
 }
 
 Slot::~Slot() {
-    for (DevBuf* b : {&queries, &qidx, &cand, &dist, &ids, &status, &aux0, &aux1, &aux2, &aux3})
+    for (DevBuf* b : {&queries, &qidx, &cand, &gcand, &counters, &dist, &ids, &status, &aux0, &aux1,
+                      &aux2, &aux3})
         b->release();
     status_h.release();
+    stage_h.release();
+    result_h.release();
     if (ev0) (void)hipEventDestroy(ev0);
     if (ev1) (void)hipEventDestroy(ev1);
     if (stream) (void)hipStreamDestroy(stream);
@@ -285,6 +288,31 @@ static int pow2_ceil(int64_t x) {
     return p;
 }
 
+// Sizes the slot's flat-scan buffers for one launch.  The merge counters
+// are zeroed when the buffer is new or a launch failed; a completed launch
+// leaves them zero.
+hipError_t prepare_flat_buffers(mans_ctx* ctx, Slot* slot, const FlatPlan& p, int64_t nq,
+                                hipStream_t st, FlatBuffers* out) {
+    size_t cnt_bytes = (size_t)nq * (size_t)(p.ngroups + 1) * sizeof(uint32_t);
+    bool fresh = cnt_bytes > slot->counters.bytes || !slot->counters.p;
+    hipError_t e = slot->cand.ensure((size_t)nq * p.nblk * p.kc * sizeof(uint64_t), ctx->fail_alloc);
+    if (e == hipSuccess)
+        e = slot->gcand.ensure((size_t)nq * p.ngroups * p.kc * sizeof(uint64_t), ctx->fail_alloc);
+    if (e == hipSuccess) e = slot->counters.ensure(cnt_bytes, ctx->fail_alloc);
+    if (e == hipSuccess) e = slot->status.ensure((size_t)nq, ctx->fail_alloc);
+    if (e != hipSuccess) return e;
+    if (fresh || slot->counters_dirty) {
+        e = hipMemsetAsync(slot->counters.p, 0, slot->counters.bytes, st);
+        if (e != hipSuccess) return e;
+        slot->counters_dirty = false;
+    }
+    out->cand = (uint64_t*)slot->cand.p;
+    out->gcand = (uint64_t*)slot->gcand.p;
+    out->counters = (uint32_t*)slot->counters.p;
+    out->status = (uint8_t*)slot->status.p;
+    return hipSuccess;
+}
+
 hipError_t fill_empty(float* dist, uint32_t* ids, int64_t count, hipStream_t s) {
     if (count <= 0) return hipSuccess;
     hipError_t e = hipMemsetD32Async((hipDeviceptr_t)dist, 0x7F7FFFFF, (size_t)count, s);
@@ -292,17 +320,43 @@ hipError_t fill_empty(float* dist, uint32_t* ids, int64_t count, hipStream_t s) 
     return e;
 }
 
+// Host <-> device copies through the slot's pinned staging buffer (a
+// pageable copy costs an extra driver-side bounce).
+hipError_t stage_to_device(Slot* s, void* dst, const void* src, size_t bytes) {
+    hipError_t e = s->stage_h.ensure(bytes);
+    if (e != hipSuccess) return e;
+    std::memcpy(s->stage_h.p, src, bytes);
+    return hipMemcpyAsync(dst, s->stage_h.p, bytes, hipMemcpyHostToDevice, s->stream);
+}
+
+hipError_t stage_from_device(Slot* s, void* dst0, const void* src0, size_t b0, void* dst1,
+                             const void* src1, size_t b1) {
+    // The previous staging upload may still be in flight on the stream.
+    hipError_t e = hipStreamSynchronize(s->stream);
+    if (e == hipSuccess) e = s->stage_h.ensure(b0 + b1);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(s->stage_h.p, src0, b0, hipMemcpyDeviceToHost, s->stream);
+    if (e == hipSuccess && b1)
+        e = hipMemcpyAsync((char*)s->stage_h.p + b0, src1, b1, hipMemcpyDeviceToHost, s->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+    if (e != hipSuccess) return e;
+    std::memcpy(dst0, s->stage_h.p, b0);
+    if (b1) std::memcpy(dst1, (char*)s->stage_h.p + b0, b1);
+    return hipSuccess;
+}
+
 // Runs the flat scan for queries already in device memory.  The proof loop
 // (kc x4 per round, exact keys past kc = 1024) mirrors the budget growth of
 // BoundedExactScan.swift:96-121.
 static int flat_search_chunk(mans_ctx* ctx, const mans_corpus* c, const float* d_q, int64_t nq,
                              int64_t k, uint32_t metric, float* d_dist, uint32_t* d_ids,
-                             hipStream_t st, Slot* slot);
+                             hipStream_t st, Slot* slot, float* h_dist, uint32_t* h_ids);
 
 // Queries go through in chunks so the grid's y extent and the candidate
 // workspace stay bounded.
 int flat_search_run(mans_ctx* ctx, const mans_corpus* c, const float* d_q, int64_t nq, int64_t k,
-                    uint32_t metric, float* d_dist, uint32_t* d_ids, hipStream_t st, Slot* slot) {
+                    uint32_t metric, float* d_dist, uint32_t* d_ids, hipStream_t st, Slot* slot,
+                    float* h_dist, uint32_t* h_ids) {
     if (metric > 2) return fail(MANS_SEARCH_FAILED, "flat scan does not support this metric");
     if (nq <= 0 || k <= 0) return MANS_OK;
     if (ctx->fail_launch) return fail(MANS_EXECUTION_FAILED, "injected launch failure");
@@ -310,7 +364,8 @@ int flat_search_run(mans_ctx* ctx, const mans_corpus* c, const float* d_q, int64
     for (int64_t q0 = 0; q0 < nq; q0 += chunk) {
         int64_t m = std::min(chunk, nq - q0);
         int rc = flat_search_chunk(ctx, c, d_q + q0 * c->dim, m, k, metric, d_dist + q0 * k,
-                                   d_ids + q0 * k, st, slot);
+                                   d_ids + q0 * k, st, slot, h_dist ? h_dist + q0 * k : nullptr,
+                                   h_ids ? h_ids + q0 * k : nullptr);
         if (rc != MANS_OK) return rc;
     }
     return MANS_OK;
@@ -318,12 +373,17 @@ int flat_search_run(mans_ctx* ctx, const mans_corpus* c, const float* d_q, int64
 
 static int flat_search_chunk(mans_ctx* ctx, const mans_corpus* c, const float* d_q, int64_t nq,
                              int64_t k, uint32_t metric, float* d_dist, uint32_t* d_ids,
-                             hipStream_t st, Slot* slot) {
+                             hipStream_t st, Slot* slot, float* h_dist, uint32_t* h_ids) {
     const int64_t n = c->n;
     const int dim = (int)c->dim;
     const int kstride = (int)k;
+    const size_t obytes = (size_t)nq * k * sizeof(float);
     if (n == 0) {
         hipError_t e = fill_empty(d_dist, d_ids, nq * k, st);
+        if (e == hipSuccess && h_dist)
+            e = hipMemcpyAsync(h_dist, d_dist, obytes, hipMemcpyDeviceToHost, st);
+        if (e == hipSuccess && h_ids)
+            e = hipMemcpyAsync(h_ids, d_ids, obytes, hipMemcpyDeviceToHost, st);
         if (e == hipSuccess) e = hipStreamSynchronize(st);
         return e == hipSuccess ? MANS_OK : hip_fail(e, "fill");
     }
@@ -345,25 +405,30 @@ static int flat_search_chunk(mans_ctx* ctx, const mans_corpus* c, const float* d
                                    hipMemcpyHostToDevice, st);
             d_qidx = (const uint32_t*)slot->qidx.p;
         }
-        if (e == hipSuccess)
-            e = slot->cand.ensure((size_t)npend * p.nblk * p.kc * sizeof(uint64_t), ctx->fail_alloc);
-        if (e == hipSuccess) e = slot->status.ensure((size_t)npend, ctx->fail_alloc);
+        FlatBuffers fb;
+        if (e == hipSuccess) e = prepare_flat_buffers(ctx, slot, p, npend, st, &fb);
         if (e == hipSuccess) e = slot->status_h.ensure((size_t)npend);
         if (e != hipSuccess) return hip_fail(e, "flat scan workspace");
+        fb.out_dist = d_dist;
+        fb.out_ids = d_ids;
         ctx->time_begin(slot, st);
-        e = launch_flat_scan(p, exact, (const float*)c->rows.p, (const float*)c->norms.p, n, dim,
-                             d_q, d_qidx, npend, (int)metric, (uint64_t*)slot->cand.p, st);
+        e = launch_flat_search(p, exact, (const float*)c->rows.p, (const float*)c->norms.p, n, dim,
+                               d_q, d_qidx, npend, (int)metric, fb, keff, kstride, st);
         ctx->time_end(slot, st, "flat_scan");
-        if (e == hipSuccess)
-            e = launch_flat_merge(p, (const float*)c->rows.p, (const float*)c->norms.p, n, dim, d_q,
-                                  d_qidx, npend, (int)metric, keff, kstride,
-                                  (const uint64_t*)slot->cand.p, d_dist, d_ids,
-                                  (uint8_t*)slot->status.p, st);
+        // Results (when the caller wants them on the host) and the proof
+        // status come back together: one synchronisation per round.
+        if (e == hipSuccess && h_dist)
+            e = hipMemcpyAsync(h_dist, d_dist, obytes, hipMemcpyDeviceToHost, st);
+        if (e == hipSuccess && h_ids)
+            e = hipMemcpyAsync(h_ids, d_ids, obytes, hipMemcpyDeviceToHost, st);
         if (e == hipSuccess)
             e = hipMemcpyAsync(slot->status_h.p, slot->status.p, (size_t)npend,
                                hipMemcpyDeviceToHost, st);
         if (e == hipSuccess) e = hipStreamSynchronize(st);
-        if (e != hipSuccess) return hip_fail(e, "flat scan");
+        if (e != hipSuccess) {
+            slot->counters_dirty = true;
+            return hip_fail(e, "flat scan");
+        }
         const uint8_t* sh = (const uint8_t*)slot->status_h.p;
         std::vector<uint32_t> next;
         for (int64_t i = 0; i < npend; ++i)
@@ -392,7 +457,8 @@ int mans_flat_search_device(mans_ctx* ctx, const mans_corpus* c, const float* d_
     SlotLease lease(ctx);
     if (!lease.slot) return fail(MANS_RESOURCE_EXHAUSTED, "could not create a HIP stream");
     hipStream_t st = stream ? (hipStream_t)stream : lease.slot->stream;
-    return flat_search_run(ctx, c, d_queries, nq, k, metric, d_out_dist, d_out_ids, st, lease.slot);
+    return flat_search_run(ctx, c, d_queries, nq, k, metric, d_out_dist, d_out_ids, st, lease.slot,
+                           nullptr, nullptr);
 }
 
 int mans_flat_search(mans_ctx* ctx, const mans_corpus* c, const float* queries, int64_t nq,
@@ -409,15 +475,16 @@ int mans_flat_search(mans_ctx* ctx, const mans_corpus* c, const float* queries, 
     hipError_t e = s->queries.ensure(qbytes, ctx->fail_alloc);
     if (e == hipSuccess) e = s->dist.ensure(obytes, ctx->fail_alloc);
     if (e == hipSuccess) e = s->ids.ensure(obytes, ctx->fail_alloc);
-    if (e == hipSuccess) e = hipMemcpyAsync(s->queries.p, queries, qbytes, hipMemcpyHostToDevice, s->stream);
+    if (e == hipSuccess) e = s->result_h.ensure(2 * obytes);
+    if (e == hipSuccess) e = stage_to_device(s, s->queries.p, queries, qbytes);
     if (e != hipSuccess) return hip_fail(e, "flat scan staging");
+    float* hd = (float*)s->result_h.p;
+    uint32_t* hi = (uint32_t*)((char*)s->result_h.p + obytes);
     int rc = flat_search_run(ctx, c, (const float*)s->queries.p, nq, k, metric, (float*)s->dist.p,
-                             (uint32_t*)s->ids.p, s->stream, s);
+                             (uint32_t*)s->ids.p, s->stream, s, hd, hi);
     if (rc != MANS_OK) return rc;
-    e = hipMemcpyAsync(out_dist, s->dist.p, obytes, hipMemcpyDeviceToHost, s->stream);
-    if (e == hipSuccess) e = hipMemcpyAsync(out_ids, s->ids.p, obytes, hipMemcpyDeviceToHost, s->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
-    if (e != hipSuccess) return hip_fail(e, "flat scan results");
+    std::memcpy(out_dist, hd, obytes);
+    std::memcpy(out_ids, hi, obytes);
     return MANS_OK;
 }
 

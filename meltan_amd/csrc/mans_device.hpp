@@ -66,9 +66,11 @@ __device__ __forceinline__ float host_distance(float dot, float qn, float vn, in
 }
 
 // Sequential dot in the order of dots.c:40-47.
+// (Unrolled so the loads are issued ahead; the additions stay in order.)
 __device__ __forceinline__ float exact_dot(const float* __restrict__ a, const float* __restrict__ b,
                                            int dim) {
     float acc = 0.0f;
+#pragma unroll 8
     for (int d = 0; d < dim; ++d) acc = acc + a[d] * b[d];
     return acc;
 }
@@ -87,8 +89,9 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
     return lane == 0 ? 0ull : (~0ull >> (64 - lane));
 }
 
-// Ascending bitonic sort of `size` (power of two) packed slots in LDS by one wave.
-__device__ inline void wave_bitonic_sort(uint64_t* buf, int size) {
+// Ascending bitonic sort of `size` (power of two) packed slots in LDS by one
+// wave, through LDS (any size).
+__device__ __forceinline__ void wave_bitonic_sort_lds(uint64_t* buf, int size) {
     const int lane = __lane_id();
     for (int k2 = 2; k2 <= size; k2 <<= 1) {
         for (int j = k2 >> 1; j > 0; j >>= 1) {
@@ -108,8 +111,91 @@ __device__ inline void wave_bitonic_sort(uint64_t* buf, int size) {
     }
 }
 
+// x from lane (lane ^ j), j a power of two below 64: DPP for j = 1, 2, 8
+// (quad permutes, and a rotate by 8 within a 16-lane row), ds_swizzle
+// (xor mode, within 32 lanes) for 4 and 16, a permute for 32.
+__device__ __forceinline__ uint32_t lane_xor32(uint32_t x, int j) {
+    switch (j) {
+    case 1: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xF, 0xF, false);
+    case 2: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xF, 0xF, false);
+    case 4: return (uint32_t)__builtin_amdgcn_ds_swizzle((int)x, 0x1F | (4 << 10));
+    case 8: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x128, 0xF, 0xF, false);
+    case 16: return (uint32_t)__builtin_amdgcn_ds_swizzle((int)x, 0x1F | (16 << 10));
+    default: return (uint32_t)__shfl_xor((int)x, j);
+    }
+}
+
+__device__ __forceinline__ uint64_t lane_xor64(uint64_t x, int j) {
+    uint32_t lo = lane_xor32((uint32_t)x, j);
+    uint32_t hi = lane_xor32((uint32_t)(x >> 32), j);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// Ascending bitonic sort of 64 * E values held in registers, element
+// i = lane + 64 e in v[e].  Exchanges across lanes use lane_xor64; those
+// within a lane are plain compares.
+template <int E>
+__device__ __forceinline__ void wave_sort_regs(uint64_t (&v)[E]) {
+    const int lane = __lane_id();
+    constexpr int N = 64 * E;
+#pragma unroll
+    for (int k2 = 2; k2 <= N; k2 <<= 1) {
+#pragma unroll
+        for (int j = k2 >> 1; j > 0; j >>= 1) {
+            if (j >= 64) {
+                const int je = j / 64;
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    const int pe = e ^ je;
+                    if (pe > e) {
+                        const bool up = ((lane + 64 * e) & k2) == 0;
+                        uint64_t a = v[e], b = v[pe];
+                        bool sw = (a > b) == up;
+                        v[e] = sw ? b : a;
+                        v[pe] = sw ? a : b;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    uint64_t b = lane_xor64(v[e], j);
+                    const bool up = ((lane + 64 * e) & k2) == 0;
+                    const bool lower = (lane & j) == 0;
+                    uint64_t mn = v[e] < b ? v[e] : b;
+                    uint64_t mx = v[e] < b ? b : v[e];
+                    v[e] = (lower == up) ? mn : mx;
+                }
+            }
+        }
+    }
+}
+
+template <int E>
+__device__ __forceinline__ void wave_sort_lds_via_regs(uint64_t* buf) {
+    const int lane = __lane_id();
+    uint64_t v[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[e] = buf[lane + 64 * e];
+    wave_sort_regs<E>(v);
+#pragma unroll
+    for (int e = 0; e < E; ++e) buf[lane + 64 * e] = v[e];
+}
+
+// Ascending bitonic sort of `size` (power of two) packed slots in LDS by one wave.
+// Sizes up to 256 are sorted in registers.
+__device__ __forceinline__ void wave_bitonic_sort(uint64_t* buf, int size) {
+    if (size == 64 || size == 128 || size == 256) {
+        if (size == 64) wave_sort_lds_via_regs<1>(buf);
+        else if (size == 128) wave_sort_lds_via_regs<2>(buf);
+        else wave_sort_lds_via_regs<4>(buf);
+        wave_sync();
+        return;
+    }
+    wave_bitonic_sort_lds(buf, size);
+}
+
 // Ascending bitonic sort of `size` (power of two) slots in LDS by the whole block.
-__device__ inline void block_bitonic_sort(uint64_t* buf, int size) {
+__device__ __forceinline__ void block_bitonic_sort(uint64_t* buf, int size) {
     const int tid = threadIdx.x, nt = blockDim.x;
     for (int k2 = 2; k2 <= size; k2 <<= 1) {
         for (int j = k2 >> 1; j > 0; j >>= 1) {
@@ -133,8 +219,8 @@ __device__ inline void block_bitonic_sort(uint64_t* buf, int size) {
 // Offers with key <= threshold are appended to an LDS buffer of `cap` slots
 // (cap a power of two, cap >= kc + 64); when the buffer cannot take another
 // full wave of offers it is sorted and cut back to kc, and the threshold
-// becomes the kc-th key.  Every slot it drops has key >= the final kc-th
-// key, which is what the lower-bound proofs downstream rely on.
+// becomes the kc-th key.  Every slot dropped has key >= the final kc-th key
+// of the stream, which is what the lower-bound proofs downstream rely on.
 struct WaveTopK {
     uint64_t* buf;
     int cap;
@@ -142,7 +228,7 @@ struct WaveTopK {
     int count;
     float thresh;
 
-    __device__ void init(uint64_t* b, int capacity, int keep) {
+    __device__ __forceinline__ void init(uint64_t* b, int capacity, int keep) {
         buf = b;
         cap = capacity;
         kc = keep;
@@ -150,7 +236,7 @@ struct WaveTopK {
         thresh = __int_as_float(0x7F800000);  // +inf
     }
 
-    __device__ void compact() {
+    __device__ __forceinline__ void compact() {
         const int lane = __lane_id();
         for (int i = count + lane; i < cap; i += 64) buf[i] = kEmptySlot;
         wave_sync();
@@ -176,15 +262,27 @@ struct WaveTopK {
         }
     }
 
+    // Offers `n` packed slots from LDS (another wave's finished list).
+    __device__ __forceinline__ void offer_slots(const uint64_t* src, int n) {
+        const int lane = __lane_id();
+        for (int base = 0; base < n; base += 64) {
+            int i = base + lane;
+            uint64_t s = i < n ? src[i] : kEmptySlot;
+            bool v = s != kEmptySlot;
+            offer(v, v ? slot_key(s) : 0.0f, slot_id(s));
+        }
+    }
+
     // Sorts the buffer; slots [0, min(count, kc)) hold the result, the rest
     // of [0, cap) is padded with kEmptySlot.
-    __device__ void finish() {
+    __device__ __forceinline__ void finish() {
         wave_sync();
         const int lane = __lane_id();
         for (int i = count + lane; i < cap; i += 64) buf[i] = kEmptySlot;
         wave_sync();
         wave_bitonic_sort(buf, cap);
         if (count > kc) count = kc;
+        if (count == kc) thresh = slot_key(buf[kc - 1]);
         for (int i = count + lane; i < cap; i += 64) buf[i] = kEmptySlot;
         wave_sync();
     }

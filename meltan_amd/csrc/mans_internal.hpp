@@ -6,11 +6,25 @@
 
 namespace mans {
 
+constexpr int kGroupBlocks = 32;  // blocks whose lists one group merge combines
+
 struct FlatPlan {
-    int kc = 0;              // candidates kept per block and per query
+    int kc = 0;              // candidates kept per wave, block, group and query
     int cap = 0;             // LDS slots per wave (power of two, >= kc + 64, >= 2 kc)
     int64_t rows_per_block = 0;
-    int nblk = 0;
+    int nblk = 0;            // blocks per query
+    int group_blocks = kGroupBlocks;
+    int ngroups = 0;         // groups per query
+};
+
+// Device buffers of one flat-scan launch.
+struct FlatBuffers {
+    uint64_t* cand = nullptr;      // nq * nblk * kc slots
+    uint64_t* gcand = nullptr;     // nq * ngroups * kc slots
+    uint32_t* counters = nullptr;  // nq * (ngroups + 1), zero before and after a launch
+    float* out_dist = nullptr;     // indexed by query id, k_stride per query
+    uint32_t* out_ids = nullptr;
+    uint8_t* status = nullptr;     // nq
 };
 
 FlatPlan plan_flat(int64_t n, int64_t nq, int kc);
@@ -19,14 +33,11 @@ int flat_cap_for(int kc);
 
 hipError_t launch_row_norms(const float* rows, int64_t n, int dim, float* out, hipStream_t s);
 
+// One launch: scan, merges, exact rescore, results and proof status.
 // exact == true forces the row-wise kernel whose keys are exact distances.
-hipError_t launch_flat_scan(const FlatPlan& p, bool exact, const float* rows, const float* norms,
-                            int64_t n, int dim, const float* queries, const uint32_t* qidx,
-                            int64_t nq, int metric, uint64_t* cand, hipStream_t s);
-
-hipError_t launch_flat_merge(const FlatPlan& p, const float* rows, const float* norms, int64_t n,
-                             int dim, const float* queries, const uint32_t* qidx, int64_t nq,
-                             int metric, int k, int k_stride, const uint64_t* cand,
-                             float* out_dist, uint32_t* out_ids, uint8_t* status, hipStream_t s);
+hipError_t launch_flat_search(const FlatPlan& p, bool exact, const float* rows, const float* norms,
+                              int64_t n, int dim, const float* queries, const uint32_t* qidx,
+                              int64_t nq, int metric, const FlatBuffers& b, int k, int k_stride,
+                              hipStream_t s);
 
 }  // namespace mans

@@ -11,6 +11,7 @@
 #include <vector>
 
 #include "mans_hip.h"
+#include "mans_internal.hpp"
 
 namespace mans {
 
@@ -37,9 +38,10 @@ struct PinnedBuf {
 struct Slot {
     hipStream_t stream = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
-    DevBuf queries, qidx, cand, dist, ids, status;
+    DevBuf queries, qidx, cand, gcand, counters, dist, ids, status;
+    bool counters_dirty = false;  // a launch failed: re-zero the merge counters
     DevBuf aux0, aux1, aux2, aux3;
-    PinnedBuf status_h;
+    PinnedBuf status_h, stage_h, result_h;  // pinned status, query staging, results
     ~Slot();
 };
 
@@ -99,8 +101,16 @@ struct SlotLease {
 };
 
 hipError_t fill_empty(float* dist, uint32_t* ids, int64_t count, hipStream_t s);
+hipError_t prepare_flat_buffers(mans_ctx* ctx, Slot* slot, const FlatPlan& p, int64_t nq,
+                                hipStream_t st, FlatBuffers* out);
+hipError_t stage_to_device(Slot* s, void* dst, const void* src, size_t bytes);
+hipError_t stage_from_device(Slot* s, void* dst0, const void* src0, size_t b0, void* dst1,
+                             const void* src1, size_t b1);
+// h_dist/h_ids (nullable, pinned) receive the results with the same
+// synchronisation that reads the proof status.
 int flat_search_run(mans_ctx* ctx, const mans_corpus* c, const float* d_q, int64_t nq, int64_t k,
-                    uint32_t metric, float* d_dist, uint32_t* d_ids, hipStream_t st, Slot* slot);
+                    uint32_t metric, float* d_dist, uint32_t* d_ids, hipStream_t st, Slot* slot,
+                    float* h_dist, uint32_t* h_ids);
 hipError_t int8_refresh_rows(mans_corpus* c, int64_t first_row, int64_t count, hipStream_t s);
 
 }  // namespace mans
