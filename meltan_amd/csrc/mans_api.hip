@@ -395,26 +395,43 @@ static int flat_search_chunk(mans_ctx* ctx, const mans_corpus* c, const float* d
     int64_t npend = nq;
     for (;;) {
         if (exact) kc = pow2_ceil(std::max(32, keff));
-        FlatPlan p = plan_flat(n, npend, kc);
-        const uint32_t* d_qidx = nullptr;
         hipError_t e = hipSuccess;
-        if (!pending.empty()) {
-            e = slot->qidx.ensure(pending.size() * sizeof(uint32_t), ctx->fail_alloc);
-            if (e == hipSuccess)
-                e = hipMemcpyAsync(slot->qidx.p, pending.data(), pending.size() * sizeof(uint32_t),
-                                   hipMemcpyHostToDevice, st);
-            d_qidx = (const uint32_t*)slot->qidx.p;
+        GemmPlan gp;
+        if (pending.empty() && !exact && plan_gemm(n, dim, npend, kc, &gp)) {
+            // First round of a batch: MFMA contraction + per-query merge.
+            e = slot->cand.ensure(gemm_lists_bytes(gp, npend), ctx->fail_alloc);
+            if (e == hipSuccess) e = slot->status.ensure((size_t)npend, ctx->fail_alloc);
+            if (e == hipSuccess) e = slot->status_h.ensure((size_t)npend);
+            if (e != hipSuccess) return hip_fail(e, "flat scan workspace");
+            FlatBuffers fb;
+            fb.out_dist = d_dist;
+            fb.out_ids = d_ids;
+            fb.status = (uint8_t*)slot->status.p;
+            ctx->time_begin(slot, st);
+            e = launch_flat_gemm(gp, (const float*)c->rows.p, (const float*)c->norms.p, n, dim, d_q,
+                                 npend, (int)metric, (uint64_t*)slot->cand.p, fb, keff, kstride, st);
+            ctx->time_end(slot, st, "flat_gemm");
+        } else {
+            FlatPlan p = plan_flat(n, npend, kc);
+            const uint32_t* d_qidx = nullptr;
+            if (!pending.empty()) {
+                e = slot->qidx.ensure(pending.size() * sizeof(uint32_t), ctx->fail_alloc);
+                if (e == hipSuccess)
+                    e = hipMemcpyAsync(slot->qidx.p, pending.data(),
+                                       pending.size() * sizeof(uint32_t), hipMemcpyHostToDevice, st);
+                d_qidx = (const uint32_t*)slot->qidx.p;
+            }
+            FlatBuffers fb;
+            if (e == hipSuccess) e = prepare_flat_buffers(ctx, slot, p, npend, st, &fb);
+            if (e == hipSuccess) e = slot->status_h.ensure((size_t)npend);
+            if (e != hipSuccess) return hip_fail(e, "flat scan workspace");
+            fb.out_dist = d_dist;
+            fb.out_ids = d_ids;
+            ctx->time_begin(slot, st);
+            e = launch_flat_search(p, exact, (const float*)c->rows.p, (const float*)c->norms.p, n,
+                                   dim, d_q, d_qidx, npend, (int)metric, fb, keff, kstride, st);
+            ctx->time_end(slot, st, "flat_scan");
         }
-        FlatBuffers fb;
-        if (e == hipSuccess) e = prepare_flat_buffers(ctx, slot, p, npend, st, &fb);
-        if (e == hipSuccess) e = slot->status_h.ensure((size_t)npend);
-        if (e != hipSuccess) return hip_fail(e, "flat scan workspace");
-        fb.out_dist = d_dist;
-        fb.out_ids = d_ids;
-        ctx->time_begin(slot, st);
-        e = launch_flat_search(p, exact, (const float*)c->rows.p, (const float*)c->norms.p, n, dim,
-                               d_q, d_qidx, npend, (int)metric, fb, keff, kstride, st);
-        ctx->time_end(slot, st, "flat_scan");
         // Results (when the caller wants them on the host) and the proof
         // status come back together: one synchronisation per round.
         if (e == hipSuccess && h_dist)

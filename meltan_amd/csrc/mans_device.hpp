@@ -19,6 +19,7 @@ constexpr int kMetricIP = 2;
 constexpr float kFltMax = 3.402823466e+38f;
 
 typedef float f4v __attribute__((ext_vector_type(4)));
+typedef float f16v __attribute__((ext_vector_type(16)));  // 32x32 MFMA accumulator
 
 // 128-bit streaming load (the corpus is read once per query batch).
 __device__ __forceinline__ f4v load_stream(const float* p) {

@@ -27,6 +27,27 @@ struct FlatBuffers {
     uint8_t* status = nullptr;     // nq
 };
 
+// Batched path: fp32 MFMA contraction with fused selection, then one merge
+// and rescore block per query.
+constexpr int kGemmMaxKc = 32;        // k <= 16: the lane lists keep 4 slots each
+constexpr int64_t kGemmMinRows = 4096;  // smaller corpora stay on the streaming scan
+struct GemmPlan {
+    int kc = 0;
+    int cap = 0;   // LDS slots per wave in the merge
+    int nseg = 0;  // row segments, a multiple of 8
+    int nqb = 0;   // blocks of 128 queries
+    int64_t rows_per_seg = 0;
+};
+// False when the batch, dimension or kc does not suit the batched path.
+bool plan_gemm(int64_t n, int dim, int64_t nq, int kc, GemmPlan* out);
+size_t gemm_lists_bytes(const GemmPlan& p, int64_t nq);
+// Writes the k results and the proof status of every query (as
+// launch_flat_search); lists: gemm_lists_bytes of workspace.
+hipError_t launch_flat_gemm(const GemmPlan& p, const float* rows, const float* norms, int64_t n,
+                            int dim, const float* queries, int64_t nq, int metric,
+                            uint64_t* lists, const FlatBuffers& b, int k, int k_stride,
+                            hipStream_t s);
+
 FlatPlan plan_flat(int64_t n, int64_t nq, int kc);
 int flat_nch_for_dim(int dim);
 int flat_cap_for(int kc);
