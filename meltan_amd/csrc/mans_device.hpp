@@ -20,6 +20,7 @@ constexpr float kFltMax = 3.402823466e+38f;
 
 typedef float f4v __attribute__((ext_vector_type(4)));
 typedef float f16v __attribute__((ext_vector_type(16)));  // 32x32 MFMA accumulator
+typedef int i4v __attribute__((ext_vector_type(4)));
 
 // 128-bit streaming load (the corpus is read once per query batch).
 __device__ __forceinline__ f4v load_stream(const float* p) {
@@ -183,12 +184,14 @@ __device__ __forceinline__ void wave_sort_lds_via_regs(uint64_t* buf) {
 }
 
 // Ascending bitonic sort of `size` (power of two) packed slots in LDS by one wave.
-// Sizes up to 256 are sorted in registers.
+// Sizes up to 256 (up to MAXREG) are sorted in registers.
+template <int MAXREG = 512>
 __device__ __forceinline__ void wave_bitonic_sort(uint64_t* buf, int size) {
-    if (size == 64 || size == 128 || size == 256) {
+    if (size == 64 || size == 128 || size == 256 || (MAXREG >= 512 && size == 512)) {
         if (size == 64) wave_sort_lds_via_regs<1>(buf);
         else if (size == 128) wave_sort_lds_via_regs<2>(buf);
-        else wave_sort_lds_via_regs<4>(buf);
+        else if (size == 256) wave_sort_lds_via_regs<4>(buf);
+        else wave_sort_lds_via_regs<MAXREG >= 512 ? 8 : 4>(buf);
         wave_sync();
         return;
     }

@@ -48,7 +48,8 @@ hipError_t launch_flat_gemm(const GemmPlan& p, const float* rows, const float* n
                             uint64_t* lists, const FlatBuffers& b, int k, int k_stride,
                             hipStream_t s);
 
-FlatPlan plan_flat(int64_t n, int64_t nq, int kc);
+// target_blocks: blocks over all queries of a launch (0: the flat scan's default).
+FlatPlan plan_flat(int64_t n, int64_t nq, int kc, int64_t target_blocks = 0);
 int flat_nch_for_dim(int dim);
 int flat_cap_for(int kc);
 

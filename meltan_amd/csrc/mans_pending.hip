@@ -6,22 +6,11 @@
 
 using namespace mans;
 
-namespace mans {
-hipError_t int8_refresh_rows(mans_corpus*, int64_t, int64_t, hipStream_t) { return hipSuccess; }
-}
-
 static int unavailable(const char* what) {
     return fail(MANS_PIPELINE_UNAVAILABLE, std::string(what) + " is not available in this build");
 }
 
 extern "C" {
-int mans_int8_search(mans_ctx*, mans_corpus*, const float*, int64_t, int64_t, uint32_t, int32_t,
-                     int64_t, float*, uint32_t*, int32_t*) { return unavailable("int8 scan"); }
-int mans_int8_search_device(mans_ctx*, mans_corpus*, const float*, int64_t, int64_t, uint32_t,
-                            int32_t, int64_t, float*, uint32_t*, void*) { return unavailable("int8 scan"); }
-int mans_int8_codes_download(mans_ctx*, mans_corpus*, int8_t*, float*, float*, float*, float*) {
-    return unavailable("int8 codes");
-}
 int mans_ivf_flat_build(mans_ctx*, const mans_corpus*, const float*, int64_t, uint32_t, mans_ivf** out) {
     if (out) *out = nullptr;
     return unavailable("IVF-flat");
