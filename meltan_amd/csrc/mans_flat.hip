@@ -158,8 +158,9 @@ __global__ __launch_bounds__(256) void flat_scan_rows(
 // whole segment (DIM / 2 values per lane).  In the 32 x 32 result a lane
 // holds one query (lane % 32) against 16 rows of the tile (row
 // 8 (v / 4) + 4 h + v % 4 for accumulator v, h = lane / 32), and keeps the
-// kGemmListLen smallest (key, row) slots it has seen in registers, sorted.
-// A tile's keys are offered while the next tile's MFMAs run.
+// C smallest (key, row) slots it has seen in registers, sorted (C = 4 for
+// kc <= 32, 8 for kc = 64).  A tile's keys are offered while the next
+// tile's MFMAs run.
 //
 // flat_lists_merge selects each query's kc smallest keys over its 2 nseg
 // lists and runs the streaming scan's exact rescore.  A row turned away by a
@@ -172,14 +173,16 @@ __global__ __launch_bounds__(256) void flat_scan_rows(
 // partial sums flushed below the smallest normal.
 constexpr int kGemmQueries = 128;  // queries per block
 constexpr int kGemmRows = 32;      // rows per tile
-constexpr int kGemmListLen = 4;    // slots per lane list
+
+// Slots per lane list for a candidate count kc.
+inline int gemm_list_len(int kc) { return kc <= 32 ? 4 : 8; }
 
 struct GemmArgs {
     int nseg;              // row segments (multiple of 8)
     int nqb;               // query blocks
     int64_t rows_per_seg;  // multiple of kGemmRows
     float abs_slack;
-    uint64_t* lists;       // [nq][nseg][2][kGemmListLen]
+    uint64_t* lists;       // [nq][nseg][2][C]
 };
 
 // LDS slices of the row tile: SL MFMA steps (2 SL values of k) per slice,
@@ -227,13 +230,12 @@ __device__ __forceinline__ void list_insert(uint64_t (&l)[C], uint64_t s) {
 // the k values of its steps as float4s: rows from LDS (row-major, padded),
 // queries once from global memory into registers.  Alternate steps
 // accumulate into two chains, so consecutive MFMAs are independent.
-template <int DIM, int METRIC>
+template <int DIM, int METRIC, int C>
 __global__ __launch_bounds__(256) void flat_gemm_f32(
     const float* __restrict__ rows, const float* __restrict__ norms, int64_t n,
     const float* __restrict__ queries, int64_t nq, BoundCoef bc, GemmArgs ga) {
     using G = GemmShape<DIM>;
     constexpr int NS = G::NS, SL = G::SL, SK = G::SK, NSLICE = G::NSLICE, SS = G::SS;
-    constexpr int C = kGemmListLen;
     extern __shared__ uint64_t lds[];
     float* xs = reinterpret_cast<float*>(lds);  // [2][32][SS]
     float* tva = xs + 2 * G::SLICE_FLOATS;      // [2][32] row norms vn
@@ -390,7 +392,7 @@ __global__ __launch_bounds__(256) void flat_gemm_f32(
 template <int NCH>
 __global__ __launch_bounds__(256) void flat_lists_merge(
     const float* __restrict__ rows, const float* __restrict__ norms, int64_t n, int dim,
-    const float* __restrict__ queries, int metric, int kc, int cap, int nlists,
+    const float* __restrict__ queries, int metric, int kc, int cap, int nlists, int list_len,
     const uint64_t* __restrict__ lists, FlatArgs fa) {
     extern __shared__ uint64_t lds[];
     __shared__ uint32_t cut_bits;
@@ -404,18 +406,18 @@ __global__ __launch_bounds__(256) void flat_lists_merge(
         const int idx = lr + 16 * c;
         qv[c] = idx < dim4 ? *reinterpret_cast<const f4v*>(qp + 4 * idx) : f4v{0.f, 0.f, 0.f, 0.f};
     }
-    const uint64_t* lq = lists + (size_t)q * nlists * kGemmListLen;
+    const uint64_t* lq = lists + (size_t)q * nlists * list_len;
     if (threadIdx.x == 0) cut_bits = 0xFFFFFFFFu;
     __syncthreads();
     // Smallest largest key over the full lists (ordered key bits).
     uint32_t mine = 0xFFFFFFFFu;
     for (int i = threadIdx.x; i < nlists; i += blockDim.x) {
-        const uint64_t last = lq[(size_t)i * kGemmListLen + kGemmListLen - 1];
+        const uint64_t last = lq[(size_t)i * list_len + list_len - 1];
         if (last != kEmptySlot) mine = min(mine, (uint32_t)(last >> 32));
     }
     atomicMin(&cut_bits, mine);
     WaveTopK sel;
-    block_select_lists(lq, (int64_t)nlists * kGemmListLen, lds, cap, kc, sel);  // ends in a barrier
+    block_select_lists(lq, (int64_t)nlists * list_len, lds, cap, kc, sel);  // ends in a barrier
     const float list_cut = cut_bits == 0xFFFFFFFFu ? kFltMax : from_ordered_bits(cut_bits);
     final_rescore_f4<NCH>(qv, rows, norms, n, dim, metric, q, lds, kc, fa, list_cut);
 }
@@ -446,16 +448,6 @@ __global__ __launch_bounds__(256) void row_norms_kernel(const float* __restrict_
 }
 
 // ---------------------------------------------------------------------------
-
-// u: the unit roundoff the fast dot products are assumed to meet.
-static BoundCoef make_bounds(int dim, double u = 1.0 / 16777216.0) {
-    const double g = (double)dim * u / (1.0 - (double)dim * u);
-    BoundCoef bc;
-    bc.eps_cos = (float)((3.0 * g * (1.0 + 3.0 * g) + 16.0 * u) * 1.0001);
-    bc.c_l2 = (float)((4.0 * g + 8.0 * u) * (1.0 + 4.0 * g) * 1.0001);
-    bc.c_ip = (float)((2.0 * g + 4.0 * u) * (1.0 + 4.0 * g) * 1.0001);
-    return bc;
-}
 
 int flat_nch_for_dim(int dim) {
     if (dim % 4 != 0) return 0;
@@ -586,32 +578,41 @@ bool plan_gemm(int64_t n, int dim, int64_t nq, int kc, GemmPlan* out) {
 }
 
 size_t gemm_lists_bytes(const GemmPlan& p, int64_t nq) {
-    return (size_t)nq * (size_t)p.nseg * 2 * kGemmListLen * sizeof(uint64_t);
+    return (size_t)nq * (size_t)p.nseg * 2 * gemm_list_len(p.kc) * sizeof(uint64_t);
+}
+
+template <int DIM, int C>
+static hipError_t launch_gemm_dim_c(const GemmPlan& p, const float* rows, const float* norms,
+                                    int64_t n, const float* queries, int64_t nq, int metric,
+                                    const GemmArgs& ga, hipStream_t s) {
+    const BoundCoef bc = make_bounds(DIM, 1.0 / 8388608.0);
+    const dim3 grid((unsigned)(p.nseg * p.nqb));
+    const size_t shmem = gemm_lds_bytes<DIM>();
+    switch (metric) {
+    case kMetricCosine:
+        hipLaunchKernelGGL((flat_gemm_f32<DIM, kMetricCosine, C>), grid, dim3(256), shmem, s, rows,
+                           norms, n, queries, nq, bc, ga);
+        break;
+    case kMetricL2:
+        hipLaunchKernelGGL((flat_gemm_f32<DIM, kMetricL2, C>), grid, dim3(256), shmem, s, rows,
+                           norms, n, queries, nq, bc, ga);
+        break;
+    case kMetricIP:
+        hipLaunchKernelGGL((flat_gemm_f32<DIM, kMetricIP, C>), grid, dim3(256), shmem, s, rows,
+                           norms, n, queries, nq, bc, ga);
+        break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
 template <int DIM>
 static hipError_t launch_gemm_dim(const GemmPlan& p, const float* rows, const float* norms,
                                   int64_t n, const float* queries, int64_t nq, int metric,
                                   const GemmArgs& ga, hipStream_t s) {
-    const BoundCoef bc = make_bounds(DIM, 1.0 / 8388608.0);
-    const dim3 grid((unsigned)(p.nseg * p.nqb));
-    const size_t shmem = gemm_lds_bytes<DIM>();
-    switch (metric) {
-    case kMetricCosine:
-        hipLaunchKernelGGL((flat_gemm_f32<DIM, kMetricCosine>), grid, dim3(256), shmem, s, rows,
-                           norms, n, queries, nq, bc, ga);
-        break;
-    case kMetricL2:
-        hipLaunchKernelGGL((flat_gemm_f32<DIM, kMetricL2>), grid, dim3(256), shmem, s, rows, norms,
-                           n, queries, nq, bc, ga);
-        break;
-    case kMetricIP:
-        hipLaunchKernelGGL((flat_gemm_f32<DIM, kMetricIP>), grid, dim3(256), shmem, s, rows, norms,
-                           n, queries, nq, bc, ga);
-        break;
-    default: return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
+    return gemm_list_len(p.kc) == 4
+               ? launch_gemm_dim_c<DIM, 4>(p, rows, norms, n, queries, nq, metric, ga, s)
+               : launch_gemm_dim_c<DIM, 8>(p, rows, norms, n, queries, nq, metric, ga, s);
 }
 
 template <int NCH>
@@ -620,7 +621,8 @@ static void launch_lists_merge(const GemmPlan& p, const float* rows, const float
                                const uint64_t* lists, const FlatArgs& fa, hipStream_t s) {
     size_t shmem = sizeof(uint64_t) * 4 * (size_t)p.cap;
     hipLaunchKernelGGL(flat_lists_merge<NCH>, dim3(1, (unsigned)nq), dim3(256), shmem, s, rows,
-                       norms, n, dim, queries, metric, p.kc, p.cap, 2 * p.nseg, lists, fa);
+                       norms, n, dim, queries, metric, p.kc, p.cap, 2 * p.nseg,
+                       gemm_list_len(p.kc), lists, fa);
 }
 
 hipError_t launch_flat_gemm(const GemmPlan& p, const float* rows, const float* norms, int64_t n,

@@ -29,7 +29,7 @@ struct FlatBuffers {
 
 // Batched path: fp32 MFMA contraction with fused selection, then one merge
 // and rescore block per query.
-constexpr int kGemmMaxKc = 32;        // k <= 16: the lane lists keep 4 slots each
+constexpr int kGemmMaxKc = 64;        // k <= 32: the lane lists keep 4 or 8 slots each
 constexpr int64_t kGemmMinRows = 4096;  // smaller corpora stay on the streaming scan
 struct GemmPlan {
     int kc = 0;

@@ -11,17 +11,6 @@ static int unavailable(const char* what) {
 }
 
 extern "C" {
-int mans_ivf_flat_build(mans_ctx*, const mans_corpus*, const float*, int64_t, uint32_t, mans_ivf** out) {
-    if (out) *out = nullptr;
-    return unavailable("IVF-flat");
-}
-int mans_kmeans(mans_ctx*, const mans_corpus*, int64_t, int64_t, uint32_t, float*) { return unavailable("k-means"); }
-int mans_ivf_flat_search(mans_ctx*, const mans_ivf*, const float*, int64_t, int64_t, int64_t, float*,
-                         uint32_t*, int32_t*) { return unavailable("IVF-flat"); }
-int mans_ivf_flat_search_device(mans_ctx*, const mans_ivf*, const float*, int64_t, int64_t, int64_t,
-                                float*, uint32_t*, void*) { return unavailable("IVF-flat"); }
-int mans_ivf_download_lists(const mans_ivf*, int64_t*, uint32_t*) { return unavailable("IVF-flat"); }
-void mans_ivf_release(mans_ivf*) {}
 int mans_ivfpq_build(mans_ctx*, const mans_corpus*, const float*, int64_t, const float*, int64_t,
                      uint32_t, mans_ivfpq** out) {
     if (out) *out = nullptr;

@@ -14,6 +14,17 @@ struct BoundCoef {
     float c_ip;     // slack = c_ip * sqrt(qn vn)
 };
 
+// Slack coefficients for dimension `dim`; u: the unit roundoff the fast dot
+// products are assumed to meet (gamma_d = d u / (1 - d u)).
+inline BoundCoef make_bounds(int dim, double u = 1.0 / 16777216.0) {
+    const double g = (double)dim * u / (1.0 - (double)dim * u);
+    BoundCoef bc;
+    bc.eps_cos = (float)((3.0 * g * (1.0 + 3.0 * g) + 16.0 * u) * 1.0001);
+    bc.c_l2 = (float)((4.0 * g + 8.0 * u) * (1.0 + 4.0 * g) * 1.0001);
+    bc.c_ip = (float)((2.0 * g + 4.0 * u) * (1.0 + 4.0 * g) * 1.0001);
+    return bc;
+}
+
 __device__ __forceinline__ float lower_key(float f, float qn, float vn, int metric,
                                            const BoundCoef& bc) {
     if (metric == kMetricIP) {
@@ -158,11 +169,15 @@ enum ProofMode : int {
 // The last block of a query: exact rescore of the kc candidates held in
 // lds[0, kc), sort by (distance, id), outputs and proof status.  qv: the
 // query chunks.  lds must hold kc + pow2(kc) slots (cap >= 2 kc, 4 caps).
+// Candidate ids index `rows`; idmap (nullable) maps them to the ids that are
+// reported and that order ties.  n: the number of rows the query could see.
+// status_idx: the status slot (default: blockIdx.y).
 template <int NCH>
 __device__ __forceinline__ void final_rescore_f4(const f4v* qv, const float* __restrict__ rows,
                                  const float* __restrict__ norms, int64_t n, int dim, int metric,
                                  uint32_t q, uint64_t* lds, int kc, const FlatArgs& fa,
-                                 float list_cut = kFltMax, int proof = kProofFlat) {
+                                 float list_cut = kFltMax, int proof = kProofFlat,
+                                 const uint32_t* idmap = nullptr, int status_idx = -1) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int grp = lane >> 4, lr = lane & 15, dim4 = dim >> 2;
     __shared__ int ncand_sh;
@@ -198,7 +213,8 @@ __device__ __forceinline__ void final_rescore_f4(const f4v* qv, const float* __r
         const float dot0 = chain_dot<NCH>(a0, qv, dim4);
         if (lr == 0 && v0)
             res[s0] = pack_slot(
-                host_distance(dot0, qn, metric == kMetricIP ? 0.0f : norms[id0], metric), id0);
+                host_distance(dot0, qn, metric == kMetricIP ? 0.0f : norms[id0], metric),
+                idmap ? idmap[id0] : id0);
     }
     __syncthreads();
     if (wave == 0) wave_bitonic_sort(res, sort_n);
@@ -231,7 +247,7 @@ __device__ __forceinline__ void final_rescore_f4(const f4v* qv, const float* __r
         } else {
             ok = all_rows || (kout > 0 && cutoff >= slot_key(res[kout - 1]));
         }
-        fa.status[blockIdx.y] = ok ? 0 : 1;
+        fa.status[status_idx >= 0 ? status_idx : (int)blockIdx.y] = ok ? 0 : 1;
     }
 }
 

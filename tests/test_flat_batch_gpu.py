@@ -1,6 +1,6 @@
 """Parity of the batched flat path (fp32 MFMA contraction + fused selection).
 
-Batches of at least 16 queries with k <= 16 at dims 64/96/128/192/256/384 go
+Batches of at least 16 queries with k <= 32 at dims 64/96/128/192/256/384 go
 through the matrix-core kernel; its keys are lower bounds, so the returned
 rows must meet the same bar as the streaming scan: distances bit-identical to
 the oracle's (dots.c order, host formulas), ids equal except on exact ties.
@@ -37,7 +37,7 @@ def test_batched_parity_dims_metrics(gpu_ctx, dim):
         norms = oracle.row_norms(corpus)
         c = gpu_ctx.upload(corpus)
         for metric in (COS, L2, IP):
-            for k in (1, 10, 16):
+            for k in (1, 10, 16, 32):
                 gd, gi, launches = _search_batched(gpu_ctx, c, queries, k, metric)
                 assert launches >= 1, "the batched kernel did not run"
                 check_flat(corpus, norms, queries, k, metric, gd, gi,
@@ -108,7 +108,7 @@ def test_batched_small_corpus_uses_streaming_path(gpu_ctx):
 
 
 def test_batched_large_k_uses_streaming_path(gpu_ctx):
-    # k > 16 needs more candidates than the batched kernel keeps per lane.
+    # k > 32 needs more candidates than the batched kernel keeps per lane.
     corpus = workloads.lcg_vectors(0, 5000, 64, seed=5)
     queries = workloads.lcg_vectors(0, 20, 64, seed=6)
     c = gpu_ctx.upload(corpus)
