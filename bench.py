@@ -1,21 +1,28 @@
 #!/usr/bin/env python3
 """Benchmark of the exact-search hot path on one MI355X.
 
-Default workload: exact top-10 cosine over 1,000,000 x 384 fp32 (the
-1,000-centre Gaussian mixture, sigma 0.3, normalised), one batch of queries
-per step, queries and results resident in HBM.  Prints ONE JSON line.
+Default: exact top-10 cosine over 1,000,000 x 384 fp32 (the 1,000-centre
+Gaussian mixture, sigma 0.3, normalised), batches of 1024 queries, queries
+and results resident in HBM.  Prints ONE JSON line whose value is the batch
+throughput; the same line carries the batch-1 throughput, the p50/p95
+single-query latency at 100,000 x 384 and, unless --quick, one entry per
+other configuration (int8 prefilter, IVF-flat, IVF-PQ).
 
-  python bench.py [--steps K] [--warmup W] [--batch B] [--workload flat]
+  python bench.py [--steps K] [--warmup W] [--batch B] [--workload flat|int8|ivf|ivfpq]
 
-A parity gate runs before any timing: a sample of queries is checked against
-the CPU oracle.  The CPU baseline (the oracle's restatement of the reference
-CPU path) is timed on a bounded sample on the host's cores in the same run.
+Every workload first checks a sample of queries against the CPU oracle
+(bit-identical results) and stops if they differ.  Throughput is timed with
+no per-kernel synchronisation; kernel durations for the roofline come from
+a separate pass with HIP events recorded on the stream the kernels run on.
+The CPU baseline (the oracle's restatement of the reference CPU path) is
+timed on a bounded sample on the host's cores in the same run.
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -27,7 +34,8 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 FP32_MFMA_TFLOPS = 157.3
-BF16_MFMA_TFLOPS = 2500.0
+METRIC = "queries/sec exact top-10 @1M×384 fp32 (batch 1/1024); p50 single-query µs @100k"
+CPU_THREADS = min(16, os.cpu_count() or 1)  # the host share of one GPU
 
 
 def log(msg: str) -> None:
@@ -41,10 +49,68 @@ def percentile_nearest_rank(samples, p):
     return s[idx]
 
 
-def parity_gate(db, norms, queries, dist, ids, k, metric):
+def measured_traffic(kernel: str, workload: str):
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (profiles/hbm_traffic.md), or None."""
+    path = ROOT / "profiles" / "hbm_traffic.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 4 and cells[0] == kernel and cells[1] == workload:
+            try:
+                return int(float(cells[2]) + float(cells[3]))
+            except ValueError:
+                return None
+    return None
+
+
+def roofline_hbm(kernel, workload, bytes_per_launch, avg_s):
+    gbs = bytes_per_launch / avg_s / 1e9
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(kernel, workload),
+            "kernel": kernel, "avg_launch_us": round(avg_s * 1e6, 2),
+            "bytes_per_launch": int(bytes_per_launch)}
+
+
+def roofline_mfma(kernel, workload, flops_per_launch, avg_s):
+    tf = flops_per_launch / avg_s / 1e12
+    return {"bound": "mfma", "achieved": round(tf, 2), "peak": FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tf / FP32_MFMA_TFLOPS, 4), "traffic": measured_traffic(kernel, workload),
+            "kernel": kernel, "avg_launch_us": round(avg_s * 1e6, 2),
+            "flops_per_launch": int(flops_per_launch)}
+
+
+def timed(step, steps, warmup, hip):
+    for w in range(warmup):
+        step(w)
+    hip.synchronize()
+    t0 = time.perf_counter()
+    for s in range(steps):
+        step(s)
+    hip.synchronize()
+    return time.perf_counter() - t0
+
+
+def kernel_avg(ctx, step, reps, names, hip):
+    """Average event-timed duration (s) per launch of each named kernel."""
+    ctx.timing_reset()
+    ctx.timing(True)
+    for s in range(reps):
+        step(s)
+    hip.synchronize()
+    ctx.timing(False)
+    out = {}
+    for name in names:
+        ms, cnt = ctx.timing_read(name)
+        out[name] = (ms / cnt / 1e3, cnt) if cnt else (None, 0)
+    return out
+
+
+def parity_flat(db, norms, queries, dist, ids, k, metric):
     from oracle import oracle
 
-    od, oi, counts = oracle.flat_search_batch(db, norms, queries, k, metric)
+    od, oi, counts = oracle.flat_search_batch(db, norms, queries, k, metric, threads=CPU_THREADS)
     for i in range(queries.shape[0]):
         kk = int(counts[i])
         if not np.array_equal(od[i, :kk], dist[i, :kk]):
@@ -54,94 +120,67 @@ def parity_gate(db, norms, queries, dist, ids, k, metric):
             raise SystemExit(f"parity gate failed: query {i} ids do not carry their distances")
 
 
-def cpu_baseline_flat(db, norms, queries, k, metric):
-    from oracle import oracle
+# ---------------------------------------------------------------------------
+# Flat exact scan (T1/T2, C2)
+# ---------------------------------------------------------------------------
 
-    threads = os.cpu_count() or 1
-    t0 = time.perf_counter()
-    oracle.flat_search_batch(db, norms, queries, k, metric, threads=threads)
-    dt = time.perf_counter() - t0
-    return {
-        "value": queries.shape[0] / dt,
-        "unit": "queries/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": (f"{queries.shape[0]} queries, exact top-{k} cosine over the same "
-                   f"{db.shape[0]}x{db.shape[1]} corpus, one task per query "
-                   f"(FlatGPUSearch.swift:754-779), scalar dots.c order, {dt:.2f} s"),
-    }
-
-
-def bench_flat(args):
+def bench_flat(args, ctx):
     import meltan_amd as M
     from meltan_amd import hip, workloads
     from oracle import oracle
 
     n, dim, k, B = args.n, 384, 10, args.batch
     metric = M.METRIC_COSINE
-    log(f"generating {n} x {dim} mixture corpus")
+    log(f"flat: generating {n} x {dim} mixture corpus")
     nq_pool = max(1024, B)
     db, q = workloads.mixture_1m_384(nq=nq_pool, n=n)
-    ctx = M.Context(0)
     corpus = ctx.upload(db)
-    log("uploaded corpus")
-
-    # parity gate on a sample
-    gd, gi = corpus.flat_search(q[:8], k, metric)
     norms = oracle.row_norms(db)
-    parity_gate(db, norms, q[:8], gd, gi, k, metric)
-    log("parity gate passed (8 queries bit-identical to the oracle)")
+    gd, gi = corpus.flat_search(q[:8], k, metric)
+    parity_flat(db, norms, q[:8], gd, gi, k, metric)
+    gd, gi = corpus.flat_search(q[:64], k, metric)  # batched path
+    parity_flat(db, norms, q[:64], gd, gi, k, metric)
+    log("flat: parity gate passed (8 single and 64 batched queries bit-identical to the oracle)")
 
     dq = hip.DeviceArray.from_numpy(q)
     dd = hip.DeviceArray((nq_pool, k), np.float32)
     di = hip.DeviceArray((nq_pool, k), np.uint32)
     stream = hip.Stream()
 
-    def step(s):
-        off = (s * B) % (nq_pool - B + 1)
-        corpus.flat_search_device(dq.offset(off * dim), B, k, metric, dd.offset(off * k),
-                                  di.offset(off * k), stream.handle)
+    def make_step(b):
+        def step(s):
+            off = (s * b) % (nq_pool - b + 1)
+            corpus.flat_search_device(dq.offset(off * dim), b, k, metric, dd.offset(off * k),
+                                      di.offset(off * k), stream.handle)
+        return step
 
-    for w in range(args.warmup):
-        step(w)
-    hip.synchronize()
-    ctx.timing_reset()
-    ctx.timing(True)
-    hip.synchronize()
-    t0 = time.perf_counter()
-    for s in range(args.steps):
-        step(s)
-    hip.synchronize()
-    t1 = time.perf_counter()
-    ctx.timing(False)
-    elapsed = t1 - t0
-    gemm_ms, gemm_launches = ctx.timing_read("flat_gemm")
-    scan_ms, scan_launches = ctx.timing_read("flat_scan")
-    if gemm_launches >= args.steps:
-        # Batched path: fp32 MFMA contraction (+ the per-query merge launch).
-        avg_s = gemm_ms / gemm_launches / 1e3
-        flops = 2.0 * B * n * dim
-        achieved = flops / avg_s / 1e12
-        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_MFMA_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(achieved / FP32_MFMA_TFLOPS, 4), "traffic": None,
-                "kernel": "flat_gemm_f32 + flat_lists_merge", "avg_launch_us": round(avg_s * 1e6, 2),
-                "flops_per_launch": flops}
-    else:
-        avg_s = scan_ms / max(scan_launches, 1) / 1e3
-        bytes_per_launch = B * (n * dim * 4 + n * 4)
-        achieved = bytes_per_launch / avg_s / 1e9
-        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "flat_scan_f4", "avg_launch_us": round(avg_s * 1e6, 2),
-                "bytes_per_launch": bytes_per_launch}
-    log(f"timed {args.steps} steps in {elapsed:.4f} s; {roof['kernel']} avg {avg_s * 1e6:.1f} us "
-        f"({gemm_launches} batched, {scan_launches} streaming launches)")
+    res = {}
+    for b, steps, warmup in ((B, args.steps, args.warmup), (1, 200, 20)):
+        step = make_step(b)
+        elapsed = timed(step, steps, warmup, hip)
+        reps = min(steps, 20)
+        kt = kernel_avg(ctx, step, reps, ["flat_gemm", "flat_merge", "flat_scan"], hip)
+        if kt["flat_gemm"][1]:
+            avg, launches = kt["flat_gemm"]
+            flops = 2.0 * (b * reps / launches) * n * dim  # queries per launch x n x d
+            roof = roofline_mfma("flat_gemm_f32<384,cosine>", f"flat_{n}x{dim}_b{b}", flops, avg)
+            roof["merge_avg_us"] = round(kt["flat_merge"][0] * 1e6, 2) if kt["flat_merge"][1] else None
+        else:
+            avg, launches = kt["flat_scan"]
+            per = b * reps / max(launches, 1)
+            roof = roofline_hbm("flat_scan_f4<6>", f"flat_{n}x{dim}_b{b}", per * n * (dim * 4 + 4), avg)
+        res[b] = {"qps": b * steps / elapsed, "ms_per_step": elapsed / steps * 1e3, "steps": steps,
+                  "warmup": warmup, "roofline": roof}
+        log(f"flat: batch {b}: {res[b]['qps']:.1f} queries/s, {roof['kernel']} "
+            f"{roof['achieved']} {roof['unit']} ({roof['frac']:.3f} of peak)")
 
     extra = {}
     if not args.quick:
-        # p50 single-query latency at 100k x 384 through the host-pointer C ABI.
+        # C2: p50 single-query latency at 100k x 384 through the host-pointer C ABI.
         db100, q100 = workloads.flat_100k(1024)
         c100 = ctx.upload(db100)
+        gd, gi = c100.flat_search(q100[:4], k, metric)
+        parity_flat(db100, oracle.row_norms(db100), q100[:4], gd, gi, k, metric)
         for i in range(50):
             c100.flat_search(q100[i:i + 1], k, metric)
         lat = []
@@ -151,55 +190,256 @@ def bench_flat(args):
             lat.append((time.perf_counter() - t) * 1e6)
         extra["p50_us_100k"] = round(percentile_nearest_rank(lat, 0.5), 2)
         extra["p95_us_100k"] = round(percentile_nearest_rank(lat, 0.95), 2)
+        for b in (32, 1024):
+            t = time.perf_counter()
+            reps = 10
+            for r in range(reps):
+                c100.flat_search(q100[:b], k, metric)
+            extra[f"qps_100k_batch{b}_host_api"] = round(b * reps / (time.perf_counter() - t), 1)
         c100.release()
 
     cpu = None
     if not args.no_cpu:
         nsample = args.cpu_queries
-        log(f"CPU baseline on {nsample} queries")
-        cpu = cpu_baseline_flat(db, norms, q[:nsample], k, metric)
-
-    qps = B * args.steps / elapsed
+        log(f"flat: CPU baseline on {nsample} queries, {CPU_THREADS} threads")
+        t0 = time.perf_counter()
+        oracle.flat_search_batch(db, norms, q[:nsample], k, metric, threads=CPU_THREADS)
+        dt = time.perf_counter() - t0
+        cpu = {"value": round(nsample / dt, 2), "unit": "queries/s", "cores": CPU_THREADS,
+               "kind": "port",
+               "sample": (f"{nsample} queries, exact top-{k} cosine over the same {n}x{dim} corpus, "
+                          f"one query per thread (FlatGPUSearch.swift:754-779), scalar dots.c "
+                          f"order, {dt:.2f} s")}
+    corpus.release()
+    main_b = res[B]
     out = {
-        "metric": "queries/sec exact top-10 @1M×384 fp32 (batch 1/1024); p50 single-query µs @100k",
-        "value": round(qps, 2),
+        "metric": METRIC,
+        "value": round(main_b["qps"], 2),
         "unit": "queries/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(elapsed / args.steps * 1e3, 4),
+        "steps": main_b["steps"],
+        "warmup": main_b["warmup"],
+        "ms_per_step": round(main_b["ms_per_step"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (1,000-centre Gaussian mixture, seeded; see meltan_amd/workloads.py)",
+        "data": "synthetic (1,000-centre Gaussian mixture, seeded; meltan_amd/workloads.py)",
         "config": {"workload": f"exact flat top-{k} cosine, {n}x{dim} fp32, batch {B}",
                    "n": n, "dim": dim, "k": k, "batch": B, "metric": "cosine"},
-        "roofline": roof,
+        "roofline": main_b["roofline"],
         "cpu_baseline": cpu,
+        "batch1": {"qps": round(res[1]["qps"], 2), "ms_per_query": round(res[1]["ms_per_step"], 4),
+                   "roofline": res[1]["roofline"]},
     }
     out.update(extra)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# int8 prefilter + fp32 rerank (C3)
+# ---------------------------------------------------------------------------
+
+def bench_int8(args, ctx):
+    import meltan_amd as M
+    from meltan_amd import hip, workloads
+    from oracle import oracle
+
+    n, dim, k, budget = 1_000_000, 384, 10, 100
+    metric = M.METRIC_COSINE
+    log("int8: 1M x 384 mixture, top-100 prefilter then rerank to top-10")
+    db, q = workloads.mixture_1m_384(nq=1024, n=n)
+    corpus = ctx.upload(db)
+    norms = oracle.row_norms(db)
+    planes = oracle.int8_build(db)
+    gd, gi, _ = corpus.int8_search(q[:2], k, metric, mode=1, budget=budget)
+    for i in range(2):
+        od, oi, _ = oracle.int8_search(db, norms, planes, q[i], k, metric, mode=1, budget=budget)
+        if not (np.array_equal(gd[i, :len(od)], od) and np.array_equal(gi[i, :len(oi)], oi)):
+            raise SystemExit("int8 parity gate failed")
+    del planes
+    dq = hip.DeviceArray.from_numpy(q)
+    dd = hip.DeviceArray((1024, k), np.float32)
+    di = hip.DeviceArray((1024, k), np.uint32)
+    stream = hip.Stream()
+    out = {"workload": f"int8 prefilter top-{budget} + exact rerank top-{k}, cosine, {n}x{dim}"}
+    for b, steps in ((1, 100), (1024, 3)):
+        def step(s, b=b):
+            off = (s * b) % (1024 - b + 1)
+            corpus.int8_search_device(dq.offset(off * dim), b, k, metric, 1, budget,
+                                      dd.offset(off * k), di.offset(off * k), stream.handle)
+        elapsed = timed(step, steps, 2, hip)
+        kt = kernel_avg(ctx, step, min(steps, 10), ["int8_scan"], hip)
+        avg, launches = kt["int8_scan"]
+        per = b * min(steps, 10) // max(launches, 1)
+        if b == 1:
+            roof = roofline_hbm("int8_scan<6>", f"int8_{n}x{dim}_b{b}", per * n * (dim + 12), avg)
+        else:
+            # A batch re-reads the codes from cache across queries: its bound is
+            # the int8 contraction (dense i8 MFMA 5.0 POP/s), which this path
+            # does not use yet.
+            ops = 2.0 * per * n * dim
+            roof = {"bound": "mfma", "achieved": round(ops / avg / 1e12, 2), "peak": 5000.0,
+                    "unit": "TOP/s", "frac": round(ops / avg / 1e12 / 5000.0, 5), "traffic": None,
+                    "kernel": "int8_scan<6>", "avg_launch_us": round(avg * 1e6, 2),
+                    "ops_per_launch": int(ops)}
+        out[f"batch{b}"] = {"qps": round(b * steps / elapsed, 1), "roofline": roof}
+        log(f"int8: batch {b}: {out[f'batch{b}']['qps']} queries/s")
+    corpus.release()
+    return out
+
+
+# ---------------------------------------------------------------------------
+# IVF-flat (C4)
+# ---------------------------------------------------------------------------
+
+def bench_ivf(args, ctx):
+    import meltan_amd as M
+    from meltan_amd import hip, workloads
+    from oracle import oracle
+
+    n, dim, nlist, k, B = 1_000_000, 128, 4096, 10, 1024
+    log("ivf: 1M x 128 mixture, device k-means (10 iterations), nlist 4096")
+    db, q = workloads.mixture_1m_128(nq=B)
+    corpus = ctx.upload(db)
+    t = time.perf_counter()
+    cents = corpus.kmeans(nlist, 10, M.METRIC_L2)
+    t_km = time.perf_counter() - t
+    t = time.perf_counter()
+    ivf = corpus.ivf_flat_build(cents, M.METRIC_L2)
+    t_build = time.perf_counter() - t
+    off, ids = ivf.lists()
+    sizes = np.diff(off)
+    part = oracle.IVFPartition.__new__(oracle.IVFPartition)
+    part.metric, part.dim, part.count, part.nlist = M.METRIC_L2, dim, n, nlist
+    part.centroids, part.cnorms = cents, oracle.row_norms(cents)
+    part.offsets, part.list_ids = off, ids
+    part.packed = np.ascontiguousarray(db[ids])
+    part.packed_norms = oracle.row_norms(part.packed)
+    dq = hip.DeviceArray.from_numpy(q)
+    dd = hip.DeviceArray((B, k), np.float32)
+    di = hip.DeviceArray((B, k), np.uint32)
+    stream = hip.Stream()
+    out = {"workload": f"IVF-flat L2 top-{k}, {n}x{dim}, nlist {nlist}, batch {B}",
+           "kmeans_s": round(t_km, 3), "build_s": round(t_build, 3)}
+    for nprobe in (4, 8, 32):
+        gd, gi, gp = ivf.search(q, k, nprobe, want_probes=True)
+        for i in (0, 1):
+            od, oi, op = part.search(q[i], k, nprobe)
+            if not (np.array_equal(gp[i], op) and np.array_equal(gd[i, :len(od)], od)):
+                raise SystemExit("IVF parity gate failed")
+        cand_rows = int(sum(sizes[gp[i]].sum() for i in range(B)))
+
+        def step(s, nprobe=nprobe):
+            ivf.search_device(dq.ptr, B, k, nprobe, dd.ptr, di.ptr, stream.handle)
+        elapsed = timed(step, 5, 1, hip)
+        kt = kernel_avg(ctx, step, 3, ["ivf_scan"], hip)
+        avg, _ = kt["ivf_scan"]
+        out[f"nprobe{nprobe}"] = {
+            "qps": round(B * 5 / elapsed, 1),
+            "candidates_per_query": round(cand_rows / B, 1),
+            "roofline": roofline_hbm("ivf_scan<2>", f"ivf_{n}x{dim}_np{nprobe}_b{B}",
+                                     cand_rows * (dim * 4 + 4 + 4), avg)}
+        log(f"ivf: nprobe {nprobe}: {out[f'nprobe{nprobe}']['qps']} queries/s")
+    ivf.release()
+    corpus.release()
+    return out
+
+
+# ---------------------------------------------------------------------------
+# IVF-PQ (C5)
+# ---------------------------------------------------------------------------
+
+def bench_ivfpq(args, ctx):
+    import meltan_amd as M
+    from meltan_amd import hip, workloads
+    from oracle import oracle
+
+    n = args.pq_n
+    dim, nlist, m, nprobe, kadc, rer, B = 96, 8192, 48, 16, 100, 10, 1024
+    log(f"ivfpq: {n} x 96 mixture, nlist {nlist}, M {m} x 8 bit, nprobe {nprobe}")
+    db, q, _ = workloads.mixture_10m_96(nq=B, n=n)
+    corpus = ctx.upload(db)
+    t = time.perf_counter()
+    coarse = corpus.kmeans(nlist, 2, M.METRIC_L2)
+    t_km = time.perf_counter() - t
+    rng = np.random.default_rng(5003)
+    books = np.ascontiguousarray(db[rng.choice(n, 256, replace=False)].reshape(256, m, 2)
+                                 .transpose(1, 0, 2)).astype(np.float32)
+    t = time.perf_counter()
+    pq = corpus.ivfpq_build(coarse, books, M.METRIC_INNER_PRODUCT)
+    t_build = time.perf_counter() - t
+    gs, gi = pq.search(q[:2], kadc, nprobe, rerank_k=rer)
+    codes, assign = pq.codes()
+    offsets, ids = oracle.ivf_lists(assign, nlist)
+    for i in range(2):
+        os_, oi = oracle.ivfpq_search(coarse, books, codes, offsets, ids, M.METRIC_INNER_PRODUCT, q[i], kadc,
+                                      nprobe, rows=db, rerank_k=rer)
+        if not (np.array_equal(gs[i], os_) and np.array_equal(gi[i], oi)):
+            raise SystemExit("IVF-PQ parity gate failed")
+    sizes = np.diff(offsets)
+    probes = [oracle.ivfpq_probe(coarse, q[i], nprobe, M.METRIC_INNER_PRODUCT)[0] for i in range(B)]
+    cand_per_query = float(np.mean([sizes[p].sum() for p in probes]))
+    del codes, db
+    dq = hip.DeviceArray.from_numpy(q)
+    dd = hip.DeviceArray((B, kadc), np.float32)
+    di = hip.DeviceArray((B, kadc), np.uint32)
+    stream = hip.Stream()
+    out = {"workload": f"IVF-PQ ADC IP, {n}x{dim}, nlist {nlist}, M {m}, nprobe {nprobe}, "
+                       f"top-{kadc} then exact rerank to {rer}, batch {B}",
+           "kmeans_s": round(t_km, 3), "build_s": round(t_build, 3),
+           "candidates_per_query": round(cand_per_query, 1)}
+    for rerank in (0, rer):
+        def step(s, rerank=rerank):
+            pq.search_device(dq.ptr, B, kadc, nprobe, rerank, dd.ptr, di.ptr, stream.handle)
+        elapsed = timed(step, 5, 1, hip)
+        kt = kernel_avg(ctx, step, 3, ["ivfpq_scan"], hip)
+        avg, _ = kt["ivfpq_scan"]
+        key = "adc_rerank" if rerank else "adc"
+        out[key] = {"qps": round(B * 5 / elapsed, 1),
+                    "roofline": roofline_hbm("ivfpq_scan", f"ivfpq_{n}x{dim}_b{B}",
+                                             B * cand_per_query * (m + 4), avg)}
+        log(f"ivfpq: {key}: {out[key]['qps']} queries/s")
+    pq.release()
+    corpus.release()
     return out
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--batch", type=int, default=1024)
     ap.add_argument("--n", type=int, default=1_000_000)
-    ap.add_argument("--workload", default="flat", choices=["flat"])
-    ap.add_argument("--quick", action="store_true", help="skip the 100k latency extra")
+    ap.add_argument("--pq-n", type=int, default=10_000_000)
+    ap.add_argument("--workload", default="flat", choices=["flat", "int8", "ivf", "ivfpq"])
+    ap.add_argument("--quick", action="store_true", help="flat only, no 100k or per-config extras")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-queries", type=int, default=64)
+    ap.add_argument("--cpu-queries", type=int, default=128)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: every scan here runs on a single MI355X and this build "
               "has no multi-GPU path; the sharded design is documented alongside the code.",
               file=sys.stderr)
         sys.exit(2)
-    out = bench_flat(args)
+    import meltan_amd as M
+
+    ctx = M.Context(0)
+    if args.workload == "flat":
+        out = bench_flat(args, ctx)
+        if not args.quick:
+            for name, fn in (("int8", bench_int8), ("ivf", bench_ivf), ("ivfpq", bench_ivfpq)):
+                try:
+                    out[name] = fn(args, ctx)
+                except SystemExit:
+                    raise
+                except Exception as exc:  # a failed extra must not hide the main line
+                    out[name] = {"error": f"{type(exc).__name__}: {exc}"}
+    else:
+        fn = {"int8": bench_int8, "ivf": bench_ivf, "ivfpq": bench_ivfpq}[args.workload]
+        out = {"metric": METRIC, "workload": args.workload}
+        out.update(fn(args, ctx))
     print(json.dumps(out), flush=True)
 
 

@@ -409,8 +409,14 @@ static int flat_search_chunk(mans_ctx* ctx, const mans_corpus* c, const float* d
             fb.status = (uint8_t*)slot->status.p;
             ctx->time_begin(slot, st);
             e = launch_flat_gemm(gp, (const float*)c->rows.p, (const float*)c->norms.p, n, dim, d_q,
-                                 npend, (int)metric, (uint64_t*)slot->cand.p, fb, keff, kstride, st);
+                                 npend, (int)metric, (uint64_t*)slot->cand.p, st);
             ctx->time_end(slot, st, "flat_gemm");
+            ctx->time_begin(slot, st);
+            if (e == hipSuccess)
+                e = launch_flat_gemm_merge(gp, (const float*)c->rows.p, (const float*)c->norms.p, n,
+                                           dim, d_q, npend, (int)metric,
+                                           (const uint64_t*)slot->cand.p, fb, keff, kstride, st);
+            ctx->time_end(slot, st, "flat_merge");
         } else {
             FlatPlan p = plan_flat(n, npend, kc);
             const uint32_t* d_qidx = nullptr;

@@ -627,8 +627,7 @@ static void launch_lists_merge(const GemmPlan& p, const float* rows, const float
 
 hipError_t launch_flat_gemm(const GemmPlan& p, const float* rows, const float* norms, int64_t n,
                             int dim, const float* queries, int64_t nq, int metric,
-                            uint64_t* lists, const FlatBuffers& b, int k, int k_stride,
-                            hipStream_t s) {
+                            uint64_t* lists, hipStream_t s) {
     GemmArgs ga;
     ga.nseg = p.nseg;
     ga.nqb = p.nqb;
@@ -647,7 +646,13 @@ hipError_t launch_flat_gemm(const GemmPlan& p, const float* rows, const float* n
     case 384: e = launch_gemm_dim<384>(p, rows, norms, n, queries, nq, metric, ga, s); break;
     default: return hipErrorInvalidValue;
     }
-    if (e != hipSuccess) return e;
+    return e;
+}
+
+hipError_t launch_flat_gemm_merge(const GemmPlan& p, const float* rows, const float* norms,
+                                  int64_t n, int dim, const float* queries, int64_t nq, int metric,
+                                  const uint64_t* lists, const FlatBuffers& b, int k, int k_stride,
+                                  hipStream_t s) {
     FlatArgs fa = {};
     fa.out_dist = b.out_dist;
     fa.out_ids = b.out_ids;

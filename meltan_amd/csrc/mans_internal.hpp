@@ -41,12 +41,17 @@ struct GemmPlan {
 // False when the batch, dimension or kc does not suit the batched path.
 bool plan_gemm(int64_t n, int dim, int64_t nq, int kc, GemmPlan* out);
 size_t gemm_lists_bytes(const GemmPlan& p, int64_t nq);
-// Writes the k results and the proof status of every query (as
-// launch_flat_search); lists: gemm_lists_bytes of workspace.
+// The contraction with the fused selection: writes the lane lists
+// (gemm_lists_bytes of workspace).
 hipError_t launch_flat_gemm(const GemmPlan& p, const float* rows, const float* norms, int64_t n,
                             int dim, const float* queries, int64_t nq, int metric,
-                            uint64_t* lists, const FlatBuffers& b, int k, int k_stride,
-                            hipStream_t s);
+                            uint64_t* lists, hipStream_t s);
+// The per-query merge, exact rescore and proof: writes the k results and the
+// proof status of every query (as launch_flat_search).
+hipError_t launch_flat_gemm_merge(const GemmPlan& p, const float* rows, const float* norms,
+                                  int64_t n, int dim, const float* queries, int64_t nq, int metric,
+                                  const uint64_t* lists, const FlatBuffers& b, int k, int k_stride,
+                                  hipStream_t s);
 
 // target_blocks: blocks over all queries of a launch (0: the flat scan's default).
 FlatPlan plan_flat(int64_t n, int64_t nq, int kc, int64_t target_blocks = 0);
