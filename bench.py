@@ -417,6 +417,9 @@ def main():
     ap.add_argument("--quick", action="store_true", help="flat only, no 100k or per-config extras")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-queries", type=int, default=128)
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="first copy MIB MiB device to device (a plain copy kernel of known size, "
+                         "the scale for rocprofv3 FETCH_SIZE / WRITE_SIZE counts)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: every scan here runs on a single MI355X and this build "
@@ -426,6 +429,16 @@ def main():
     import meltan_amd as M
 
     ctx = M.Context(0)
+    if args.calibrate_copy > 0:
+        from meltan_amd import hip
+
+        nb = args.calibrate_copy << 20
+        src, dst = hip.DeviceArray(nb, np.uint8), hip.DeviceArray(nb, np.uint8)
+        dst.copy_from(src)
+        hip.synchronize()
+        log(f"calibration copy: {nb} bytes device to device")
+        src.free()
+        dst.free()
     if args.workload == "flat":
         out = bench_flat(args, ctx)
         if not args.quick:

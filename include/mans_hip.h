@@ -178,7 +178,8 @@ void mans_ivfpq_release(mans_ivfpq *pq);
 /* Kernel timing with HIP events on the stream each kernel runs on.
  * enable != 0 starts accumulating; read returns the summed milliseconds and
  * launch count of the named kernel class ("flat_scan", "flat_gemm",
- * "int8_scan", "ivf_scan", "ivfpq_scan") since the last reset. */
+ * "flat_merge", "int8_scan", "ivf_scan", "ivfpq_scan") since the last
+ * reset.  While enabled, each timed launch is waited for. */
 int mans_timing_enable(mans_ctx *ctx, int enable);
 int mans_timing_read(mans_ctx *ctx, const char *kernel, double *total_ms, int64_t *launches);
 int mans_timing_reset(mans_ctx *ctx);

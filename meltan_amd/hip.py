@@ -73,6 +73,11 @@ class DeviceArray:
     def offset(self, elements: int) -> int:
         return self.ptr + elements * self.dtype.itemsize
 
+    def copy_from(self, other: "DeviceArray") -> None:
+        """Device-to-device copy of min(nbytes) bytes (a plain copy kernel)."""
+        _ok(hip().hipMemcpy(self.ptr, other.ptr, min(self.nbytes, other.nbytes), D2D),
+            "hipMemcpy D2D")
+
     def free(self) -> None:
         if self.ptr:
             hip().hipFree(self.ptr)
