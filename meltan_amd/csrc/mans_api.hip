@@ -80,8 +80,8 @@ void PinnedBuf::release() {
 }
 
 Slot::~Slot() {
-    for (DevBuf* b : {&queries, &qidx, &cand, &gcand, &counters, &dist, &ids, &status, &aux0, &aux1,
-                      &aux2, &aux3})
+    for (DevBuf* b : {&queries, &qidx, &cand, &gcand, &counters, &dist, &ids, &status, &heads,
+                      &aux0, &aux1, &aux2, &aux3})
         b->release();
     status_h.release();
     stage_h.release();
@@ -301,6 +301,11 @@ hipError_t prepare_flat_buffers(mans_ctx* ctx, Slot* slot, const FlatPlan& p, in
     if (e == hipSuccess) e = slot->counters.ensure(cnt_bytes, ctx->fail_alloc);
     if (e == hipSuccess) e = slot->status.ensure((size_t)nq, ctx->fail_alloc);
     if (e != hipSuccess) return e;
+    if (p.fast) {
+        e = slot->heads.ensure((size_t)nq * p.nblk * sizeof(uint64_t), ctx->fail_alloc);
+        if (e != hipSuccess) return e;
+        out->heads = (uint64_t*)slot->heads.p;
+    }
     if (fresh || slot->counters_dirty) {
         e = hipMemsetAsync(slot->counters.p, 0, slot->counters.bytes, st);
         if (e != hipSuccess) return e;

@@ -172,6 +172,51 @@ __device__ __forceinline__ void wave_sort_regs(uint64_t (&v)[E]) {
     }
 }
 
+__device__ __forceinline__ uint64_t shfl64(uint64_t x, int src) {
+    uint32_t lo = (uint32_t)__shfl((int)(uint32_t)x, src);
+    uint32_t hi = (uint32_t)__shfl((int)(uint32_t)(x >> 32), src);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// Bitonic merge (half-cleaners J, J/2, ..., 1) of one slot per lane:
+// every aligned run of 2J lanes holding a bitonic sequence ends up ascending.
+template <int J>
+__device__ __forceinline__ uint64_t wave_bitonic_merge(uint64_t v) {
+    const int lane = __lane_id();
+#pragma unroll
+    for (int j = J; j > 0; j >>= 1) {
+        uint64_t b = lane_xor64(v, j);
+        const bool lower = (lane & j) == 0;
+        uint64_t mn = v < b ? v : b;
+        uint64_t mx = v < b ? b : v;
+        v = lower ? mn : mx;
+    }
+    return v;
+}
+
+// The kc (32 or 64) smallest slots of four ascending lists of kc slots
+// (lists[w * stride + i], padded with kEmptySlot), ascending in lanes
+// [0, kc) of the calling wave.  For sorted A and B, min(A[i], B[kc-1-i])
+// is a bitonic sequence holding the kc smallest of both lists.
+__device__ __forceinline__ uint64_t wave_top_of_four(const uint64_t* lists, int stride, int kc) {
+    const int lane = __lane_id();
+    if (kc == 64) {
+        uint64_t a = lists[lane], b = lists[stride + 63 - lane];
+        uint64_t c = lists[2 * stride + lane], d = lists[3 * stride + 63 - lane];
+        uint64_t x = wave_bitonic_merge<32>(a < b ? a : b);
+        uint64_t y = wave_bitonic_merge<32>(c < d ? c : d);
+        uint64_t yr = shfl64(y, 63 - lane);
+        return wave_bitonic_merge<32>(x < yr ? x : yr);
+    }
+    // kc == 32: lists 0 and 1 merge in lanes 0-31, lists 2 and 3 in 32-63.
+    const int h = lane & 31;
+    const int off = lane >= 32 ? 2 * stride : 0;
+    uint64_t a = lists[off + h], b = lists[off + stride + 31 - h];
+    uint64_t x = wave_bitonic_merge<16>(a < b ? a : b);
+    uint64_t xr = shfl64(x, lane ^ 63);  // lane i < 32 gets lane 63 - i
+    return wave_bitonic_merge<16>(x < xr ? x : xr);
+}
+
 template <int E>
 __device__ __forceinline__ void wave_sort_lds_via_regs(uint64_t* buf) {
     const int lane = __lane_id();
@@ -187,11 +232,11 @@ __device__ __forceinline__ void wave_sort_lds_via_regs(uint64_t* buf) {
 // Sizes up to 256 (up to MAXREG) are sorted in registers.
 template <int MAXREG = 512>
 __device__ __forceinline__ void wave_bitonic_sort(uint64_t* buf, int size) {
-    if (size == 64 || size == 128 || size == 256 || (MAXREG >= 512 && size == 512)) {
+    if (size >= 64 && size <= MAXREG && (size & (size - 1)) == 0) {
         if (size == 64) wave_sort_lds_via_regs<1>(buf);
-        else if (size == 128) wave_sort_lds_via_regs<2>(buf);
-        else if (size == 256) wave_sort_lds_via_regs<4>(buf);
-        else wave_sort_lds_via_regs<MAXREG >= 512 ? 8 : 4>(buf);
+        else if (MAXREG >= 128 && size == 128) wave_sort_lds_via_regs<MAXREG >= 128 ? 2 : 1>(buf);
+        else if (MAXREG >= 256 && size == 256) wave_sort_lds_via_regs<MAXREG >= 256 ? 4 : 1>(buf);
+        else if (MAXREG >= 512) wave_sort_lds_via_regs<MAXREG >= 512 ? 8 : 1>(buf);
         wave_sync();
         return;
     }
@@ -225,16 +270,29 @@ __device__ __forceinline__ void block_bitonic_sort(uint64_t* buf, int size) {
 // full wave of offers it is sorted and cut back to kc, and the threshold
 // becomes the kc-th key.  Every slot dropped has key >= the final kc-th key
 // of the stream, which is what the lower-bound proofs downstream rely on.
-struct WaveTopK {
+// CAP > 0: the capacity is fixed at CAP (only the sorts of CAP and 64 slots
+// are compiled in).
+template <int CAP = 0>
+struct WaveTopKT {
     uint64_t* buf;
     int cap;
     int kc;
     int count;
     float thresh;
 
+    __device__ __forceinline__ void sort_first(int size) {
+        if constexpr (CAP > 0) {
+            if (size == 64) wave_sort_lds_via_regs<1>(buf);
+            else wave_bitonic_sort<CAP>(buf, CAP);
+            wave_sync();
+        } else {
+            wave_bitonic_sort(buf, size);
+        }
+    }
+
     __device__ __forceinline__ void init(uint64_t* b, int capacity, int keep) {
         buf = b;
-        cap = capacity;
+        cap = CAP > 0 ? CAP : capacity;
         kc = keep;
         count = 0;
         thresh = __int_as_float(0x7F800000);  // +inf
@@ -244,7 +302,7 @@ struct WaveTopK {
         const int lane = __lane_id();
         for (int i = count + lane; i < cap; i += 64) buf[i] = kEmptySlot;
         wave_sync();
-        wave_bitonic_sort(buf, cap);
+        sort_first(cap);
         if (count >= kc) {
             count = kc;
             thresh = slot_key(buf[kc - 1]);
@@ -278,18 +336,21 @@ struct WaveTopK {
     }
 
     // Sorts the buffer; slots [0, min(count, kc)) hold the result, the rest
-    // of [0, cap) is padded with kEmptySlot.
+    // of [0, cap) is padded with kEmptySlot.  (At most 64 slots in use: only
+    // the first 64 are sorted.)
     __device__ __forceinline__ void finish() {
         wave_sync();
         const int lane = __lane_id();
         for (int i = count + lane; i < cap; i += 64) buf[i] = kEmptySlot;
         wave_sync();
-        wave_bitonic_sort(buf, cap);
+        sort_first(count <= 64 ? 64 : cap);
         if (count > kc) count = kc;
         if (count == kc) thresh = slot_key(buf[kc - 1]);
         for (int i = count + lane; i < cap; i += 64) buf[i] = kEmptySlot;
         wave_sync();
     }
 };
+
+using WaveTopK = WaveTopKT<0>;
 
 }  // namespace mans

@@ -7,6 +7,12 @@
 namespace mans {
 
 constexpr int kGroupBlocks = 32;  // blocks whose lists one group merge combines
+// Threshold merge of the flat scan: used when kc <= kFastMaxKc and a query
+// has at most kFastMaxBlocks block lists.
+constexpr int kFastMaxKc = 64;
+constexpr int kFastMaxBlocks = 8192;
+constexpr int kFastListCap = 1024;  // lists whose head is <= the threshold, held in LDS
+constexpr int kFastCandCap = 512;   // candidate slots the merge block sorts in LDS
 
 struct FlatPlan {
     int kc = 0;              // candidates kept per wave, block, group and query
@@ -15,6 +21,7 @@ struct FlatPlan {
     int nblk = 0;            // blocks per query
     int group_blocks = kGroupBlocks;
     int ngroups = 0;         // groups per query
+    bool fast = false;       // threshold merge (kc <= kFastMaxKc, nblk <= kFastMaxBlocks)
 };
 
 // Device buffers of one flat-scan launch.
@@ -22,6 +29,7 @@ struct FlatBuffers {
     uint64_t* cand = nullptr;      // nq * nblk * kc slots
     uint64_t* gcand = nullptr;     // nq * ngroups * kc slots
     uint32_t* counters = nullptr;  // nq * (ngroups + 1), zero before and after a launch
+    uint64_t* heads = nullptr;     // nq * nblk (threshold merge)
     float* out_dist = nullptr;     // indexed by query id, k_stride per query
     uint32_t* out_ids = nullptr;
     uint8_t* status = nullptr;     // nq

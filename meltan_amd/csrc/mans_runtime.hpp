@@ -39,6 +39,7 @@ struct Slot {
     hipStream_t stream = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     DevBuf queries, qidx, cand, gcand, counters, dist, ids, status;
+    DevBuf heads;                 // block heads of the flat scan's threshold merge
     bool counters_dirty = false;  // a launch failed: re-zero the merge counters
     DevBuf aux0, aux1, aux2, aux3;
     PinnedBuf status_h, stage_h, result_h;  // pinned status, query staging, results

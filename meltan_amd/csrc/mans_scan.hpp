@@ -25,22 +25,20 @@ inline BoundCoef make_bounds(int dim, double u = 1.0 / 16777216.0) {
     return bc;
 }
 
+// Branch-free (all three keys, then a select): a branch here would split
+// the scan loop into blocks across which the compiler does not keep the
+// next step's loads in flight.
 __device__ __forceinline__ float lower_key(float f, float qn, float vn, int metric,
                                            const BoundCoef& bc) {
-    if (metric == kMetricIP) {
-        float s = sqrtf(qn * vn);
-        return -f - s * bc.c_ip;
-    }
-    if (metric == kMetricL2) {
-        float s = sqrtf(qn * vn);
-        float dd = qn - 2.0f * f + vn;
-        dd = dd > 0.0f ? dd : 0.0f;
-        return dd - (qn + vn + 2.0f * s) * bc.c_l2;
-    }
-    if (vn == 0.0f) return 1.0f - bc.eps_cos;  // both paths give exactly 1
-    float s = sqrtf(qn * vn);
-    if (s < 1.001e-10f) return -1.0f;  // near the 1e-10 branch of the formula
-    return (1.0f - f / s) - bc.eps_cos;
+    const float s = sqrtf(qn * vn);
+    const float k_ip = -f - s * bc.c_ip;
+    float dd = qn - 2.0f * f + vn;
+    dd = dd > 0.0f ? dd : 0.0f;
+    const float k_l2 = dd - (qn + vn + 2.0f * s) * bc.c_l2;
+    float k_cos = (1.0f - f / s) - bc.eps_cos;
+    k_cos = s < 1.001e-10f ? -1.0f : k_cos;            // near the 1e-10 branch of the formula
+    k_cos = vn == 0.0f ? 1.0f - bc.eps_cos : k_cos;    // both paths give exactly 1
+    return metric == kMetricIP ? k_ip : (metric == kMetricL2 ? k_l2 : k_cos);
 }
 
 // Per-launch outputs and merge bookkeeping (indexed by blockIdx.y).
@@ -55,6 +53,9 @@ struct FlatArgs {
     int k_stride;
     int group_blocks;
     int ngroups;
+    // Threshold merge (flat scan, kc <= 64): one head per block list.
+    uint64_t* heads = nullptr;    // [nq][nblk]
+    int fast = 0;
 };
 
 // Lists passed between blocks are written and read with device-scope
@@ -68,15 +69,16 @@ __device__ __forceinline__ uint64_t load_shared_slot(const uint64_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// All threads call this after their store_shared_slot writes; returns true
-// (in every thread) in the block that arrives last at `counter` (expected
-// arrivals: `total`).  The workgroup release waits until this block's
-// device-scope stores are complete, the barrier makes that true for every
-// wave, and only then is the arrival counted, so the last block to arrive
-// finds every list at the coherence point.
+// All threads call this after their store_shared_slot writes (and device-
+// scope atomics); returns true (in every thread) in the block that arrives
+// last at `counter` (expected arrivals: `total`).  Each wave first waits
+// until its vector memory operations are complete (a workgroup-scope
+// release fence does not wait for them on this target), the barrier makes
+// that true for every wave, and only then is the arrival counted, so the
+// last block to arrive finds every list at the coherence point.
 __device__ __forceinline__ bool block_arrive_last(uint32_t* counter, uint32_t total) {
     __shared__ int last;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (threadIdx.x == 0)
         last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
@@ -88,8 +90,9 @@ __device__ __forceinline__ bool block_arrive_last(uint32_t* counter, uint32_t to
 // Block-wide selection of the kc smallest of `total` slots in global memory
 // (lists written by other blocks); result sorted in lds[0, kc) (wave 0's
 // buffer).
+template <class Sel>
 __device__ __forceinline__ void block_select_lists(const uint64_t* src, int64_t total, uint64_t* lds,
-                                                   int cap, int kc, WaveTopK& sel) {
+                                                   int cap, int kc, Sel& sel) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nt = blockDim.x;
     const int nw = nt >> 6;
     sel.init(lds + wave * cap, cap, kc);
@@ -157,6 +160,270 @@ __device__ __forceinline__ float chain_dot(const f4v* a, const f4v* b, int dim4)
         }
     }
     return __shfl(acc, row0 | last);
+}
+
+// Threshold merge, step 1 (the scan kernel, every block): fold the block's
+// four sorted wave lists (lds, stride cap) into its kc best (kc 32 or 64)
+// and write them and the block's head (its smallest slot) with plain stores;
+// the merge kernel reads them after the scan kernel has completed.  (No
+// atomics: device-scope atomics queue behind the scan's memory traffic.)
+__device__ __forceinline__ void flat_fast_block_out(const uint64_t* lds, int cap, int kc,
+                                                    const FlatArgs& fa) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nblk = gridDim.x;
+    __syncthreads();  // the four wave lists are final
+    if (wave == 0) {
+        const uint64_t v = wave_top_of_four(lds, cap, kc);
+        uint64_t* cand_q = fa.cand + (int64_t)blockIdx.y * nblk * kc;
+        if (lane < kc) cand_q[(int64_t)blockIdx.x * kc + lane] = v;
+        if (lane == 0) fa.heads[(int64_t)blockIdx.y * nblk + blockIdx.x] = v;
+    }
+}
+
+// Threshold merge, step 2 (one block of 256 threads per query): the kc best
+// of the nblk block lists (cand_q, kc slots each) and their heads.  The heads
+// are spread over 2 kc buckets (list b -> bucket b % 2 kc) and T is the kc-th
+// smallest bucket minimum: the minima are heads of distinct lists, so at
+// least kc slots are <= T and the query's kc best are the kc smallest slots
+// <= T; only lists whose head is <= T hold such slots.  Those slots are
+// gathered in LDS and sorted.  If more than kFastListCap lists or
+// kFastCandCap slots qualify (many equal keys), every list is selected over
+// instead.  Result: the kc best ascending in lds[0, kc) (kEmptySlot past the
+// last candidate).
+template <class Sel>
+__device__ __forceinline__ void flat_fast_merge_lists(uint64_t* lds, int cap, int kc, int nblk,
+                                                      const uint64_t* __restrict__ cand_q,
+                                                      const uint64_t* __restrict__ heads_q,
+                                                      Sel& sel) {
+    __shared__ uint64_t bucket_sh[2 * kFastMaxKc];
+    __shared__ uint64_t thr_sh;
+    __shared__ int nlist_sh, ncand_sh;
+    __shared__ uint16_t qlist[kFastListCap];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nb = 2 * kc;
+    if (tid < nb) bucket_sh[tid] = kEmptySlot;
+    if (tid == 0) {
+        nlist_sh = 0;
+        ncand_sh = 0;
+    }
+    constexpr int kHeads = 4;  // heads per thread and round
+    uint64_t hv[kHeads];
+#pragma unroll
+    for (int i = 0; i < kHeads; ++i) {
+        const int b = tid + 256 * i;
+        hv[i] = b < nblk ? heads_q[b] : kEmptySlot;
+    }
+    __syncthreads();
+    for (int h0 = 0; h0 < nblk; h0 += 256 * kHeads) {
+        if (h0 > 0) {
+#pragma unroll
+            for (int i = 0; i < kHeads; ++i) {
+                const int b = h0 + tid + 256 * i;
+                hv[i] = b < nblk ? heads_q[b] : kEmptySlot;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kHeads; ++i)
+            if (hv[i] != kEmptySlot)
+                atomicMin((unsigned long long*)&bucket_sh[(h0 + tid + 256 * i) % nb],
+                          (unsigned long long)hv[i]);
+    }
+    __syncthreads();
+    if (wave == 0) {
+        uint64_t t;
+        if (kc == 32) {
+            uint64_t v[1];
+            v[0] = bucket_sh[lane];
+            wave_sort_regs<1>(v);
+            t = shfl64(v[0], 31);
+        } else {
+            uint64_t v[2];
+            v[0] = bucket_sh[lane];
+            v[1] = bucket_sh[64 + lane];
+            wave_sort_regs<2>(v);
+            t = shfl64(v[0], 63);
+        }
+        if (lane == 0) thr_sh = t;  // kEmptySlot: fewer than kc lists, all qualify
+    }
+    __syncthreads();
+    const uint64_t T = thr_sh;
+    for (int h0 = 0; h0 < nblk; h0 += 256 * kHeads) {
+        if (h0 > 0) {
+#pragma unroll
+            for (int i = 0; i < kHeads; ++i) {
+                const int b = h0 + tid + 256 * i;
+                hv[i] = b < nblk ? heads_q[b] : kEmptySlot;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kHeads; ++i) {
+            const bool pass = hv[i] != kEmptySlot && hv[i] <= T;
+            const uint64_t m = __ballot(pass);
+            if (m == 0) continue;
+            int base = 0;
+            if (lane == 0) base = atomicAdd(&nlist_sh, __popcll(m));
+            base = __shfl(base, 0);
+            const int pos = base + __popcll(m & lanemask_lt());
+            if (pass && pos < kFastListCap) qlist[pos] = (uint16_t)(h0 + tid + 256 * i);
+        }
+    }
+    __syncthreads();
+    const int nl = nlist_sh;
+    if (nl > kFastListCap) {  // more qualifying lists than the queue holds
+        block_select_lists(cand_q, (int64_t)nblk * kc, lds, cap, kc, sel);
+        return;
+    }
+    const int total = nl * kc;
+    const int lkc = kc == 32 ? 5 : 6;
+    constexpr int kAhead = 8;
+    for (int e0 = 0; e0 < total; e0 += 256 * kAhead) {
+        uint64_t sv[kAhead];
+#pragma unroll
+        for (int u = 0; u < kAhead; ++u) {
+            const int e = e0 + 256 * u + tid;
+            sv[u] = e < total ? cand_q[(int64_t)qlist[e >> lkc] * kc + (e & (kc - 1))] : kEmptySlot;
+        }
+#pragma unroll
+        for (int u = 0; u < kAhead; ++u) {
+            const bool pass = sv[u] != kEmptySlot && sv[u] <= T;
+            const uint64_t m = __ballot(pass);
+            if (m == 0) continue;
+            int base = 0;
+            if (lane == 0) base = atomicAdd(&ncand_sh, __popcll(m));
+            base = __shfl(base, 0);
+            const int pos = base + __popcll(m & lanemask_lt());
+            if (pass && pos < kFastCandCap) lds[pos] = sv[u];
+        }
+    }
+    __syncthreads();
+    const int nc = ncand_sh;
+    if (nc > kFastCandCap) {
+        block_select_lists(cand_q, (int64_t)nblk * kc, lds, cap, kc, sel);
+        return;
+    }
+    int size = 64;
+    while (size < nc) size <<= 1;
+    for (int i = nc + tid; i < size; i += 256) lds[i] = kEmptySlot;
+    __syncthreads();
+    if (wave == 0) wave_bitonic_sort<128>(lds, size);
+    __syncthreads();
+}
+
+// LDS the threshold merge's rescore needs beyond lds[0, 128): the query
+// (up to 512 floats) and two 32-row pieces of 32 floats per row (rows padded
+// to 36 floats, so the lanes' 16-byte reads spread over the banks).
+constexpr int kRescoreRows = 32;
+constexpr int kRescorePiece = 32;
+constexpr int kRescoreStride = 36;
+constexpr size_t kFastLdsBytes =
+    128 * sizeof(uint64_t) + (512 + 2 * kRescoreRows * kRescoreStride) * sizeof(float);
+
+// Exact rescore for the threshold merge (kc <= 64, candidates ascending in
+// lds[0, kc)).  Lane c of wave 0 runs candidate c's whole dot product in the
+// dots.c order, and lane 32 the query's own q.q; the rows reach LDS in
+// pieces of 32 floats, loaded by the whole block (eight pieces in flight)
+// and written one piece ahead of the lanes that read them.  32
+// candidates per pass (two passes for kc = 64).  qp: the query in global
+// memory (read with scalar loads).  Wave 0 then sorts the results; outputs
+// and the proof as final_rescore_f4 (flat proof).
+template <int NCH, bool FULL>
+__device__ __forceinline__ void final_rescore_fast(const float* __restrict__ qp,
+                                                   const float* __restrict__ rows,
+                                                   const float* __restrict__ norms, int64_t n,
+                                                   int dim, int metric, uint32_t q, uint64_t* lds,
+                                                   int kc, const FlatArgs& fa, int status_idx) {
+    constexpr int kMaxPieces = 2 * NCH;  // dim <= 64 NCH
+    constexpr int kWindow = kMaxPieces < 8 ? kMaxPieces : 8;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int dim4 = FULL ? 16 * NCH : (dim >> 2);
+    const int npieces = FULL ? kMaxPieces : (dim + kRescorePiece - 1) / kRescorePiece;
+    const uint64_t* top = lds;
+    uint64_t* res = lds + 64;
+    float* qs = reinterpret_cast<float*>(lds + 128);
+    float* stage = qs + 512;
+    const int ncand = __popcll(__ballot(lane < kc && top[lane] != kEmptySlot));
+    for (int i = tid; i < dim4; i += blockDim.x)
+        *reinterpret_cast<f4v*>(qs + 4 * i) = *reinterpret_cast<const f4v*>(qp + 4 * i);
+    const int r = tid >> 3, u = tid & 7;  // the row and float4 this thread stages
+    float qn = 0.0f;
+    for (int pass = 0; pass * kRescoreRows < ncand; ++pass) {
+        const int c = pass * kRescoreRows + r;
+        const bool rv = c < ncand;
+        const uint32_t id = rv ? slot_id(top[c]) : 0u;
+        const float* rp = rows + (int64_t)id * dim;
+        auto load_piece = [&](int pc) {
+            const int off = kRescorePiece * pc + 4 * u;
+            const bool in = rv && (FULL || off < dim);
+            const f4v t = *reinterpret_cast<const f4v*>(rp + (in ? off : 0));
+            return in ? t : f4v{0.f, 0.f, 0.f, 0.f};
+        };
+        f4v v[kWindow];  // pieces in flight: piece pc lives in v[pc % kWindow]
+#pragma unroll
+        for (int pc = 0; pc < kWindow; ++pc) v[pc] = load_piece(pc);
+        const int cl = pass * kRescoreRows + lane;  // the candidate lane `lane` rescores
+        float acc = 0.0f;
+#pragma unroll
+        for (int pc = 0; pc < kMaxPieces; ++pc) {
+            if (!FULL && pc >= npieces) break;
+            float* buf = stage + (pc & 1) * kRescoreRows * kRescoreStride;
+            *reinterpret_cast<f4v*>(buf + r * kRescoreStride + 4 * u) = v[pc % kWindow];
+            if (pc + kWindow < kMaxPieces) v[pc % kWindow] = load_piece(pc + kWindow);
+            __syncthreads();
+            if (wave == 0 && lane <= kRescoreRows) {
+                const float* xr = lane < kRescoreRows ? buf + lane * kRescoreStride
+                                                      : qs + kRescorePiece * pc;
+                const float* yr = qp + kRescorePiece * pc;  // uniform: scalar loads
+#pragma unroll
+                for (int i = 0; i < kRescorePiece / 4; ++i) {
+                    if (!FULL && kRescorePiece * pc + 4 * i >= dim) break;
+                    const f4v x = *reinterpret_cast<const f4v*>(xr + 4 * i);
+                    const f4v y = *reinterpret_cast<const f4v*>(yr + 4 * i);
+                    acc = acc + x.x * y.x;
+                    acc = acc + x.y * y.y;
+                    acc = acc + x.z * y.z;
+                    acc = acc + x.w * y.w;
+                    // at most four row reads ahead of the chain (registers)
+                    if (i == 3) __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        }
+        if (wave == 0) {
+            if (pass == 0) qn = metric == kMetricIP ? 0.0f : __shfl(acc, kRescoreRows);
+            if (lane < kRescoreRows) {
+                uint64_t rs = kEmptySlot;
+                if (cl < ncand) {
+                    const uint32_t cid = slot_id(top[cl]);
+                    rs = pack_slot(host_distance(acc, qn, metric == kMetricIP ? 0.0f : norms[cid], metric),
+                                   cid);
+                }
+                res[cl] = rs;
+            }
+        }
+        __syncthreads();  // the stage buffers are reused by the next pass
+    }
+    if (wave == 0) {
+        uint64_t w[1];
+        w[0] = lane < ncand ? res[lane] : kEmptySlot;
+        wave_sort_regs<1>(w);
+        res[lane] = w[0];
+    }
+    __syncthreads();
+    const int kout = fa.k < ncand ? fa.k : ncand;
+    for (int i = tid; i < fa.k_stride; i += blockDim.x) {
+        float dv = kFltMax;
+        uint32_t oid = kEmptyId;
+        if (i < kout) {
+            oid = slot_id(res[i]);
+            dv = slot_key(res[i]);
+        }
+        fa.out_dist[(int64_t)q * fa.k_stride + i] = dv;
+        fa.out_ids[(int64_t)q * fa.k_stride + i] = oid;
+    }
+    if (tid == 0) {
+        const float cutoff = ncand > 0 ? slot_key(top[ncand - 1]) : 0.0f;
+        const bool ok = (int64_t)ncand >= n || (kout > 0 && cutoff >= slot_key(res[kout - 1]));
+        fa.status[status_idx] = ok ? 0 : 1;
+    }
 }
 
 // Proof applied by final_rescore_f4 to the rescored candidates.

@@ -219,3 +219,37 @@ def test_flat_1m_full_size_properties(gpu_ctx):
     norms = oracle.row_norms(db)
     gd, gi = c.flat_search(q[:4], 10, COS)
     check_flat(db, norms, q[:4], 10, COS, gd, gi, "1M")
+
+
+def test_flat_threshold_merge_paths(gpu_ctx):
+    # Single queries and small batches (below the batched path) merge the
+    # block lists by threshold: few candidates on random rows; thousands of
+    # equal keys (a duplicated row) overflow the candidate buffer and take
+    # the full selection; corpora with fewer block lists than candidates
+    # take every list.
+    print("flat threshold merge", flush=True)
+    dim = 64
+    db = workloads.lcg_vectors(0, 200_000, dim, seed=4242)
+    dup = db.copy()
+    pos = np.random.default_rng(7).choice(200_000, 5000, replace=False)
+    dup[pos] = db[123]
+    same = np.repeat(db[5:6], 200_000, axis=0)  # every key ties: the full selection
+    q = workloads.lcg_vectors(0, 3, dim, seed=4243)
+    qd = np.concatenate([db[123:124] + 1e-3 * q[:1], q[1:]]).astype(np.float32)
+    for corpus, queries, what in ((db, q, "random"), (dup, qd, "duplicates"), (same, q, "same")):
+        norms = oracle.row_norms(corpus)
+        c = gpu_ctx.upload(corpus)
+        for metric in (COS, L2, IP):
+            for k in (1, 10, 32):
+                for b in (1, 3):
+                    gd, gi = c.flat_search(queries[:b], k, metric)
+                    check_flat(corpus, norms, queries[:b], k, metric, gd, gi,
+                               f"{what} m{metric} k{k} b{b}")
+        c.release()
+    for n in (700, 3000):
+        small = db[:n].copy()
+        c = gpu_ctx.upload(small)
+        for k in (10, 32):
+            gd, gi = c.flat_search(q, k, COS)
+            check_flat(small, oracle.row_norms(small), q, k, COS, gd, gi, f"n{n} k{k}")
+        c.release()
