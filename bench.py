@@ -168,7 +168,9 @@ def bench_flat(args, ctx):
         else:
             avg, launches = kt["flat_scan"]
             per = b * reps / max(launches, 1)
-            roof = roofline_hbm("flat_scan_f4<6>", f"flat_{n}x{dim}_b{b}", per * n * (dim * 4 + 4), avg)
+            # The event pair brackets the scan and its threshold merge.
+            roof = roofline_hbm("flat_scan_f4<6> + flat_fast_merge<6>", f"flat_{n}x{dim}_b{b}",
+                                per * n * (dim * 4 + 4), avg)
         res[b] = {"qps": b * steps / elapsed, "ms_per_step": elapsed / steps * 1e3, "steps": steps,
                   "warmup": warmup, "roofline": roof}
         log(f"flat: batch {b}: {res[b]['qps']:.1f} queries/s, {roof['kernel']} "
