@@ -254,37 +254,42 @@ def bench_int8(args, ctx):
     corpus = ctx.upload(db)
     norms = oracle.row_norms(db)
     planes = oracle.int8_build(db)
-    gd, gi, _ = corpus.int8_search(q[:2], k, metric, mode=1, budget=budget)
+    gd, gi, _ = corpus.int8_search(q[:2], k, metric, mode=1, budget=budget)   # streaming scan
+    bd, bi, _ = corpus.int8_search(q[:64], k, metric, mode=1, budget=budget)  # i8 MFMA batch
     for i in range(2):
         od, oi, _ = oracle.int8_search(db, norms, planes, q[i], k, metric, mode=1, budget=budget)
-        if not (np.array_equal(gd[i, :len(od)], od) and np.array_equal(gi[i, :len(oi)], oi)):
-            raise SystemExit("int8 parity gate failed")
+        for rd, ri in ((gd, gi), (bd, bi)):
+            if not (np.array_equal(rd[i, :len(od)], od) and np.array_equal(ri[i, :len(oi)], oi)):
+                raise SystemExit("int8 parity gate failed")
     del planes
     dq = hip.DeviceArray.from_numpy(q)
     dd = hip.DeviceArray((1024, k), np.float32)
     di = hip.DeviceArray((1024, k), np.uint32)
     stream = hip.Stream()
     out = {"workload": f"int8 prefilter top-{budget} + exact rerank top-{k}, cosine, {n}x{dim}"}
-    for b, steps in ((1, 100), (1024, 3)):
+    for b, steps in ((1, 100), (1024, 10)):
         def step(s, b=b):
             off = (s * b) % (1024 - b + 1)
             corpus.int8_search_device(dq.offset(off * dim), b, k, metric, 1, budget,
                                       dd.offset(off * k), di.offset(off * k), stream.handle)
         elapsed = timed(step, steps, 2, hip)
-        kt = kernel_avg(ctx, step, min(steps, 10), ["int8_scan"], hip)
-        avg, launches = kt["int8_scan"]
-        per = b * min(steps, 10) // max(launches, 1)
+        kt = kernel_avg(ctx, step, min(steps, 10), ["int8_scan", "int8_gemm", "int8_merge"], hip)
         if b == 1:
+            avg, launches = kt["int8_scan"]
+            per = b * min(steps, 10) // max(launches, 1)
             roof = roofline_hbm("int8_scan<6>", f"int8_{n}x{dim}_b{b}", per * n * (dim + 12), avg)
         else:
-            # A batch re-reads the codes from cache across queries: its bound is
-            # the int8 contraction (dense i8 MFMA 5.0 POP/s), which this path
-            # does not use yet.
-            ops = 2.0 * per * n * dim
+            # The batch is a 1024 x 1e6 x 384 int8 contraction on i8 MFMA
+            # (dense peak 5.0 POP/s) with the key epilogue fused into it.
+            avg, launches = kt["int8_gemm"]
+            ops = 2.0 * b * n * dim
             roof = {"bound": "mfma", "achieved": round(ops / avg / 1e12, 2), "peak": 5000.0,
-                    "unit": "TOP/s", "frac": round(ops / avg / 1e12 / 5000.0, 5), "traffic": None,
-                    "kernel": "int8_scan<6>", "avg_launch_us": round(avg * 1e6, 2),
-                    "ops_per_launch": int(ops)}
+                    "unit": "TOP/s", "frac": round(ops / avg / 1e12 / 5000.0, 5),
+                    "traffic": measured_traffic("int8_gemm<12>", f"int8_{n}x{dim}_b{b}"),
+                    "kernel": "int8_gemm<12,cosine>", "avg_launch_us": round(avg * 1e6, 2),
+                    "ops_per_launch": int(ops),
+                    "merge_avg_us": round(kt["int8_merge"][0] * 1e6, 2) if kt["int8_merge"][1] else None,
+                    "reselect_scan_launches": kt["int8_scan"][1]}
         out[f"batch{b}"] = {"qps": round(b * steps / elapsed, 1), "roofline": roof}
         log(f"int8: batch {b}: {out[f'batch{b}']['qps']} queries/s")
     corpus.release()

@@ -21,6 +21,7 @@ constexpr float kFltMax = 3.402823466e+38f;
 typedef float f4v __attribute__((ext_vector_type(4)));
 typedef float f16v __attribute__((ext_vector_type(16)));  // 32x32 MFMA accumulator
 typedef int i4v __attribute__((ext_vector_type(4)));
+typedef int i16v __attribute__((ext_vector_type(16)));    // 32x32 i8 MFMA accumulator
 
 // 128-bit streaming load (the corpus is read once per query batch).
 __device__ __forceinline__ f4v load_stream(const float* p) {

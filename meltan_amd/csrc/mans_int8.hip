@@ -20,6 +20,7 @@
 //     proof-checked search returns the exact flat scan's result, which is
 //     what a proven reference round returns.
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -292,6 +293,345 @@ static void launch_int8_scan(const FlatPlan& p, const Int8Planes& pl, const floa
                        p.rows_per_block, proof, fa);
 }
 
+// ---------------------------------------------------------------------------
+// Batched queries: the code x code contraction on i8 MFMA
+// (v_mfma_i32_32x32x32_i8), with the reference keys and the selection fused
+// into the epilogue, so the nq x n key matrix is never written.
+//
+// Block: 4 waves and 128 queries (32 per wave) over one segment of rows.
+// Rows are the MFMA A operand, 64 per stage (two 32-row tiles) staged
+// through LDS (double-buffered, rows padded to an odd number of 16-byte
+// units so the 32 lanes of a half-wave hit distinct banks); queries are the
+// B operand and stay in registers (16 code bytes per lane per 32-byte
+// k-step).  A and B use the same byte layout, so the hardware pairs code
+// i of a row with code i of the query; the integer sums are exact in any
+// order, so the dots equal the reference's i8 dot bit for bit.  In the
+// 32 x 32 result a lane holds one query (lane % 32) against 16 rows of a
+// tile (row 8 (v / 4) + 4 h + v % 4 for accumulator v, h = lane / 32).
+// Each lane keeps the C smallest (key, row) slots it has seen in registers;
+// a key enters only when it beats the lane's largest slot, which after the
+// first rows is rare.  A stage's keys are offered while the next stage's
+// MFMAs run.
+//
+// int8_lists_merge then selects each query's kc smallest slots over its
+// 2 nseg lists.  A row a full list turned away has a slot above that list's
+// largest, so the selection equals the streaming scan's (the kc smallest
+// slots of all rows) whenever the kc-th selected slot is <= the smallest
+// largest slot of the full lists; otherwise the query is selected again by
+// the streaming scan at the same kc.
+constexpr int kI8Queries = 128;  // queries per block
+constexpr int kI8Rows = 64;      // rows per stage
+constexpr int kI8List = 8;       // slots per lane list
+constexpr int kI8GemmMaxKc = 256;
+
+struct I8GemmArgs {
+    int nseg;              // row segments (multiple of 8)
+    int nqb;               // query blocks
+    int64_t rows_per_seg;  // multiple of kI8Rows
+    uint64_t* lists;       // [nq][nseg][2][kI8List]
+};
+
+// KS 32-byte k-steps per row: the code stride is 32 KS or 32 KS - 16 (the
+// last 16 bytes of each LDS row and of the query are then zero).
+template <int KS>
+struct I8Shape {
+    static constexpr int KB = 32 * KS;        // k bytes per row in LDS
+    static constexpr int RS = KB + 16;        // LDS row pitch: an odd number of 16-byte units
+    static constexpr int STAGE = kI8Rows * RS;
+    static constexpr int CHUNKS = kI8Rows * KB / 16;
+    static constexpr int LOADS = (CHUNKS + 255) / 256;  // 16-byte chunks per thread per stage
+};
+
+template <int KS>
+size_t i8gemm_lds_bytes() {
+    return 2 * (size_t)I8Shape<KS>::STAGE + sizeof(float) * 3 * 3 * kI8Rows;
+}
+
+template <int C>
+__device__ __forceinline__ void lane_list_insert(uint64_t (&l)[C], uint64_t s) {
+    uint64_t below = l[0];
+    l[0] = s < l[0] ? s : l[0];
+#pragma unroll
+    for (int i = 1; i < C; ++i) {
+        const uint64_t cur = l[i];
+        const uint64_t m = s > below ? s : below;
+        l[i] = m < cur ? m : cur;
+        below = cur;
+    }
+}
+
+// grid: nseg * nqb blocks (1-D); block 256.  Block b serves segment
+// 8 (b / (8 nqb)) + b % 8 and query block (b % (8 nqb)) / 8: the query
+// blocks of one segment share b % 8, which places them on one XCD, so the
+// segment's codes are read from HBM once into that XCD's L2.
+template <int KS, int METRIC>
+__global__ __launch_bounds__(256) void int8_gemm(Int8Planes pl, int64_t n,
+                                                 const int8_t* __restrict__ qcodes,
+                                                 const Int8QueryCoef* __restrict__ coefs, int64_t nq,
+                                                 I8GemmArgs ga) {
+    using G = I8Shape<KS>;
+    constexpr int C = kI8List;
+    extern __shared__ uint64_t lds[];
+    int8_t* xs = reinterpret_cast<int8_t*>(lds);               // [2][64][RS]
+    float* cf = reinterpret_cast<float*>(xs + 2 * G::STAGE);   // [3][3][64]: u, w, normSq|invSqrt
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = lane >> 5, col = lane & 31;
+    const int stride = pl.stride;
+    const int row_chunks = stride >> 4;  // 16-byte code chunks per row in memory
+
+    const int b = blockIdx.x, grp = 8 * ga.nqb;
+    const int seg = 8 * (b / grp) + (b % 8);
+    const int qb = (b % grp) / 8;
+
+    // Lanes past the batch compute with query 0; their keys are never offered.
+    const int64_t qid = (int64_t)qb * kI8Queries + wave * 32 + col;
+    const bool qvalid = qid < nq;
+    i4v qreg[KS];
+    {
+        const int8_t* qp = qcodes + (qvalid ? qid : 0) * stride;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            const int ch = 2 * s + h;
+            qreg[s] = ch < row_chunks ? *reinterpret_cast<const i4v*>(qp + 16 * ch) : i4v{0, 0, 0, 0};
+        }
+    }
+    const Int8QueryCoef coef = coefs[qvalid ? qid : 0];
+    uint64_t lst[C];
+#pragma unroll
+    for (int i = 0; i < C; ++i) lst[i] = kEmptySlot;
+
+    const int64_t seg0 = (int64_t)seg * ga.rows_per_seg;
+    const int64_t seg1 = seg0 + ga.rows_per_seg < n ? seg0 + ga.rows_per_seg : n;
+    const int64_t nst = seg1 > seg0 ? (seg1 - seg0 + kI8Rows - 1) / kI8Rows : 0;
+
+    // The LDS pad chunk of each row (a stride of 32 KS - 16) stays zero.
+    if (row_chunks < 2 * KS) {
+        for (int r = tid; r < 2 * kI8Rows; r += 256)
+            *reinterpret_cast<i4v*>(xs + (r / kI8Rows) * G::STAGE + (r % kI8Rows) * G::RS +
+                                    16 * (2 * KS - 1)) = i4v{0, 0, 0, 0};
+    }
+
+    // Rows past the segment's end load the segment's last row (their keys
+    // are never offered), so the loads need no branch.
+    i4v pre[G::LOADS];
+    auto load_stage = [&](int64_t st) {
+#pragma unroll
+        for (int u = 0; u < G::LOADS; ++u) {
+            const int e = tid + 256 * u;
+            const int r = e / (2 * KS), c = e % (2 * KS);
+            int64_t row = seg0 + st * kI8Rows + r;
+            row = row < seg1 ? row : seg1 - 1;
+            const int cc = c < row_chunks ? c : row_chunks - 1;
+            pre[u] = __builtin_nontemporal_load(
+                reinterpret_cast<const i4v*>(pl.codes + row * stride + 16 * cc));
+        }
+    };
+    auto store_stage = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < G::LOADS; ++u) {
+            const int e = tid + 256 * u;
+            const int r = e / (2 * KS), c = e % (2 * KS);
+            if ((G::CHUNKS % 256 == 0 || e < G::CHUNKS) && c < row_chunks)
+                *reinterpret_cast<i4v*>(xs + buf * G::STAGE + r * G::RS + 16 * c) = pre[u];
+        }
+    };
+    auto store_coef = [&](int64_t st) {
+        if (tid < kI8Rows) {
+            int64_t row = seg0 + st * kI8Rows + tid;
+            row = row < seg1 ? row : seg1 - 1;
+            float* c = cf + (int)(st % 3) * 3 * kI8Rows;
+            c[tid] = pl.u[row];
+            c[kI8Rows + tid] = pl.w[row];
+            c[2 * kI8Rows + tid] = METRIC == kMetricL2 ? pl.normsq[row] : pl.invsqrt[row];
+        }
+    };
+    // Offers stage st's 32 keys per lane (st < 0: nothing).
+    auto offer = [&](const i16v& a0, const i16v& a1, int64_t st) {
+        if (st < 0) return;
+        const float* c = cf + (int)(st % 3) * 3 * kI8Rows;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int m = 32 * t + 8 * (v >> 2) + 4 * h + (v & 3);
+                const int64_t row = seg0 + st * kI8Rows + m;
+                const float dot = (float)(t == 0 ? a0[v] : a1[v]);
+                const float pn = c[2 * kI8Rows + m];
+                const float key = int8_key(METRIC, coef, dot, c[m], c[kI8Rows + m], pn, pn);
+                const uint64_t s = (qvalid && row < seg1) ? pack_slot(key, (uint32_t)row) : kEmptySlot;
+                if (s < lst[C - 1]) lane_list_insert<C>(lst, s);
+            }
+        }
+    };
+
+    if (nst > 0) {
+        load_stage(0);
+        store_stage(0);
+        store_coef(0);
+    }
+    __syncthreads();
+    int buf = 0;
+    i16v prev0 = {}, prev1 = {};
+    for (int64_t st = 0; st < nst; ++st) {
+        // Prefetch the next stage (past the last one, reload the last).
+        load_stage(st + 1 < nst ? st + 1 : st);
+        const int8_t* xa = xs + buf * G::STAGE + col * G::RS + 16 * h;
+        const int8_t* xb = xa + 32 * G::RS;
+        i16v acc0 = {}, acc1 = {};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            const i4v a0 = *reinterpret_cast<const i4v*>(xa + 32 * s);
+            const i4v a1 = *reinterpret_cast<const i4v*>(xb + 32 * s);
+            acc0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, qreg[s], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, qreg[s], acc1, 0, 0, 0);
+        }
+        // The previous stage's keys, while this stage's MFMAs run.
+        offer(prev0, prev1, st - 1);
+        if (st + 1 < nst) {
+            store_stage(buf ^ 1);  // last read before the previous barrier
+            store_coef(st + 1);
+        }
+        __syncthreads();
+        buf ^= 1;
+        prev0 = acc0;
+        prev1 = acc1;
+    }
+    offer(prev0, prev1, nst - 1);
+    if (qvalid) {
+        uint64_t* out = ga.lists + (((size_t)qid * ga.nseg + seg) * 2 + h) * C;
+#pragma unroll
+        for (int i = 0; i < C; ++i) out[i] = lst[i];
+    }
+}
+
+// grid (1, nq): one block per query selects the kc smallest slots over its
+// 2 nseg lists, then the exact rescore in the dots.c order and the proof
+// (or none) of the streaming int8 scan; the status is kStatusReselect when
+// the lists cannot show the selection is the kc smallest.
+template <int NCH>
+__global__ __launch_bounds__(256) void int8_lists_merge(
+    const float* __restrict__ rows, const float* __restrict__ norms, int64_t n, int dim,
+    const float* __restrict__ queries, int metric, int kc, int cap, int nlists,
+    const uint64_t* __restrict__ lists, int proof, FlatArgs fa) {
+    extern __shared__ uint64_t lds[];
+    __shared__ unsigned long long cut;
+    const int lr = threadIdx.x & 15;
+    const uint32_t q = blockIdx.y;
+    const int dim4 = dim >> 2;
+    const float* qp = queries + (int64_t)q * dim;
+    f4v qv[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const int idx = lr + 16 * c;
+        qv[c] = idx < dim4 ? *reinterpret_cast<const f4v*>(qp + 4 * idx) : f4v{0.f, 0.f, 0.f, 0.f};
+    }
+    const uint64_t* lq = lists + (size_t)q * nlists * kI8List;
+    if (threadIdx.x == 0) cut = kEmptySlot;
+    __syncthreads();
+    unsigned long long mine = kEmptySlot;
+    for (int i = threadIdx.x; i < nlists; i += blockDim.x) {
+        const uint64_t last = lq[(size_t)i * kI8List + kI8List - 1];
+        mine = last < mine ? last : mine;  // a full list's largest slot
+    }
+    atomicMin(&cut, mine);
+    WaveTopK sel;
+    block_select_lists(lq, (int64_t)nlists * kI8List, lds, cap, kc, sel);  // ends in a barrier
+    final_rescore_f4<NCH>(qv, rows, norms, n, dim, metric, q, lds, kc, fa, kFltMax, proof, nullptr,
+                          -1, (uint64_t)cut);
+}
+
+static bool i8gemm_ks(int stride, int* ks) {
+    const int k = (stride + 31) / 32;
+    switch (k) {
+    case 2: case 3: case 4: case 6: case 8: case 12: *ks = k; return true;
+    default: return false;
+    }
+}
+
+struct I8GemmPlan {
+    int ks = 0;
+    int nseg = 0;
+    int nqb = 0;
+    int64_t rows_per_seg = 0;
+};
+
+static bool plan_i8gemm(int64_t n, int stride, int64_t nq, int64_t kc, I8GemmPlan* out) {
+    static const int64_t min_batch = [] {
+        const char* e = std::getenv("MANS_I8GEMM_MIN_BATCH");
+        return e ? std::max<int64_t>(1, std::atoll(e)) : (int64_t)16;
+    }();
+    static const int64_t target = [] {
+        const char* e = std::getenv("MANS_I8GEMM_BLOCKS");
+        return e ? std::max<int64_t>(8, std::atoll(e)) : (int64_t)2048;
+    }();
+    I8GemmPlan p;
+    if (!i8gemm_ks(stride, &p.ks) || kc > kI8GemmMaxKc || nq < min_batch) return false;
+    p.nqb = (int)((nq + kI8Queries - 1) / kI8Queries);
+    // About `target` blocks, a multiple of 8 segments of >= 1024 rows each.
+    int64_t nseg = (target + p.nqb - 1) / p.nqb;
+    nseg = (nseg + 7) / 8 * 8;
+    int64_t max_seg = n / 1024 / 8 * 8;
+    if (nseg > max_seg) nseg = max_seg;
+    if (nseg < 8) nseg = 8;
+    const int64_t rps = (n + nseg - 1) / nseg;
+    p.rows_per_seg = (rps + kI8Rows - 1) / kI8Rows * kI8Rows;
+    p.nseg = (int)nseg;
+    *out = p;
+    return true;
+}
+
+template <int KS>
+static void launch_i8gemm_ks(const I8GemmPlan& p, const Int8Planes& pl, int64_t n,
+                             const int8_t* qcodes, const Int8QueryCoef* coefs, int64_t nq,
+                             int metric, const I8GemmArgs& ga, hipStream_t s) {
+    const dim3 grid((unsigned)(p.nseg * p.nqb));
+    const size_t shmem = i8gemm_lds_bytes<KS>();
+    switch (metric) {
+    case kMetricCosine:
+        hipLaunchKernelGGL((int8_gemm<KS, kMetricCosine>), grid, dim3(256), shmem, s, pl, n, qcodes,
+                           coefs, nq, ga);
+        break;
+    case kMetricL2:
+        hipLaunchKernelGGL((int8_gemm<KS, kMetricL2>), grid, dim3(256), shmem, s, pl, n, qcodes,
+                           coefs, nq, ga);
+        break;
+    default:
+        hipLaunchKernelGGL((int8_gemm<KS, kMetricIP>), grid, dim3(256), shmem, s, pl, n, qcodes,
+                           coefs, nq, ga);
+        break;
+    }
+}
+
+static hipError_t launch_i8gemm(const I8GemmPlan& p, const Int8Planes& pl, int64_t n,
+                                const int8_t* qcodes, const Int8QueryCoef* coefs, int64_t nq,
+                                int metric, uint64_t* lists, hipStream_t s) {
+    I8GemmArgs ga;
+    ga.nseg = p.nseg;
+    ga.nqb = p.nqb;
+    ga.rows_per_seg = p.rows_per_seg;
+    ga.lists = lists;
+    switch (p.ks) {
+    case 2: launch_i8gemm_ks<2>(p, pl, n, qcodes, coefs, nq, metric, ga, s); break;
+    case 3: launch_i8gemm_ks<3>(p, pl, n, qcodes, coefs, nq, metric, ga, s); break;
+    case 4: launch_i8gemm_ks<4>(p, pl, n, qcodes, coefs, nq, metric, ga, s); break;
+    case 6: launch_i8gemm_ks<6>(p, pl, n, qcodes, coefs, nq, metric, ga, s); break;
+    case 8: launch_i8gemm_ks<8>(p, pl, n, qcodes, coefs, nq, metric, ga, s); break;
+    case 12: launch_i8gemm_ks<12>(p, pl, n, qcodes, coefs, nq, metric, ga, s); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+template <int NCH>
+static void launch_i8_merge(const I8GemmPlan& p, const float* rows, const float* norms, int64_t n,
+                            int dim, const float* queries, int64_t nq, int metric, int kc,
+                            const uint64_t* lists, int proof, const FlatArgs& fa, hipStream_t s) {
+    const int cap = flat_cap_for(kc);
+    const size_t shmem = sizeof(uint64_t) * 4 * (size_t)cap;
+    hipLaunchKernelGGL(int8_lists_merge<NCH>, dim3(1, (unsigned)nq), dim3(256), shmem, s, rows,
+                       norms, n, dim, queries, metric, kc, cap, 2 * p.nseg, lists, proof, fa);
+}
+
 // Copies `count` rows of `width` floats: dst[i] = src[idx[i]].
 __global__ void gather_rows_kernel(const float* __restrict__ src, const uint32_t* __restrict__ idx,
                                    int64_t count, int width, float* __restrict__ dst) {
@@ -426,8 +766,128 @@ static int int8_search_run(mans_ctx* ctx, mans_corpus* c, const float* d_q, int6
 
     int64_t kc = mode == 0 ? std::max<int64_t>(256, 16 * (int64_t)keff) : budget;
     kc = std::min<int64_t>(kc, n);
+    const int proof = mode == 0 ? kProofMargin : kProofNone;
+    const float* rows = (const float*)c->rows.p;
+    const float* norms = (const float*)c->norms.p;
+
+    // One streaming round over `idx` (empty: every query) at candidate count
+    // kc; appends the queries whose proof failed to `grow`.
+    auto stream_round = [&](const std::vector<uint32_t>& idx, int64_t kc, bool timed,
+                            std::vector<uint32_t>& grow) -> int {
+        const int64_t cnt = idx.empty() ? nq : (int64_t)idx.size();
+        static const int64_t target = [] {
+            const char* e = std::getenv("MANS_INT8_BLOCKS");
+            return e ? std::max<int64_t>(1, std::atoll(e)) : (int64_t)512;
+        }();
+        FlatPlan p = plan_flat(n, cnt, (int)kc, target);
+        const uint32_t* d_qidx = nullptr;
+        hipError_t e = hipSuccess;
+        if (!idx.empty()) {
+            e = slot->qidx.ensure(idx.size() * sizeof(uint32_t), ctx->fail_alloc);
+            if (e == hipSuccess)
+                e = hipMemcpyAsync(slot->qidx.p, idx.data(), idx.size() * sizeof(uint32_t),
+                                   hipMemcpyHostToDevice, st);
+            d_qidx = (const uint32_t*)slot->qidx.p;
+        }
+        FlatBuffers fb;
+        if (e == hipSuccess) e = prepare_flat_buffers(ctx, slot, p, cnt, st, &fb);
+        if (e == hipSuccess) e = slot->status_h.ensure((size_t)cnt);
+        if (e != hipSuccess) return hip_fail(e, "int8 scan workspace");
+        FlatArgs fa = {};
+        fa.cand = fb.cand;
+        fa.gcand = fb.gcand;
+        fa.counters = fb.counters;
+        fa.out_dist = d_dist;
+        fa.out_ids = d_ids;
+        fa.status = fb.status;
+        fa.k = keff;
+        fa.k_stride = (int)k;
+        fa.group_blocks = p.group_blocks;
+        fa.ngroups = p.ngroups;
+        if (timed) ctx->time_begin(slot, st);
+        switch (nch) {
+        case 1: launch_int8_scan<1>(p, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, proof, fa, st); break;
+        case 2: launch_int8_scan<2>(p, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, proof, fa, st); break;
+        case 3: launch_int8_scan<3>(p, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, proof, fa, st); break;
+        case 4: launch_int8_scan<4>(p, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, proof, fa, st); break;
+        case 6: launch_int8_scan<6>(p, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, proof, fa, st); break;
+        case 8: launch_int8_scan<8>(p, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, proof, fa, st); break;
+        default: return fail(MANS_PIPELINE_UNAVAILABLE, "int8 scan: unsupported dim");
+        }
+        e = hipGetLastError();
+        ctx->time_end(slot, st, "int8_scan");
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(slot->status_h.p, fb.status, (size_t)cnt, hipMemcpyDeviceToHost, st);
+        if (e == hipSuccess) e = hipStreamSynchronize(st);
+        if (e != hipSuccess) {
+            slot->counters_dirty = true;
+            return hip_fail(e, "int8 scan");
+        }
+        const uint8_t* sh = (const uint8_t*)slot->status_h.p;
+        for (int64_t i = 0; i < cnt; ++i) {
+            const uint32_t qi = idx.empty() ? (uint32_t)i : idx[i];
+            rounds[qi] += 1;
+            if (sh[i]) grow.push_back(qi);
+        }
+        return MANS_OK;
+    };
+
+    // The first round of a batch on i8 MFMA; queries whose lists cannot
+    // show an exact selection repeat the round on the streaming scan.
+    auto gemm_round = [&](const I8GemmPlan& gp, int64_t kc, std::vector<uint32_t>& grow) -> int {
+        const size_t lbytes = (size_t)nq * gp.nseg * 2 * kI8List * sizeof(uint64_t);
+        hipError_t e = slot->cand.ensure(lbytes, ctx->fail_alloc);
+        if (e == hipSuccess) e = slot->status.ensure((size_t)nq, ctx->fail_alloc);
+        if (e == hipSuccess) e = slot->status_h.ensure((size_t)nq);
+        if (e != hipSuccess) return hip_fail(e, "int8 batch workspace");
+        uint64_t* lists = (uint64_t*)slot->cand.p;
+        ctx->time_begin(slot, st);
+        e = launch_i8gemm(gp, pl, n, qcodes, coefs, nq, (int)metric, lists, st);
+        ctx->time_end(slot, st, "int8_gemm");
+        FlatArgs fa = {};
+        fa.out_dist = d_dist;
+        fa.out_ids = d_ids;
+        fa.status = (uint8_t*)slot->status.p;
+        fa.k = keff;
+        fa.k_stride = (int)k;
+        ctx->time_begin(slot, st);
+        if (e == hipSuccess) {
+            switch (nch) {
+            case 1: launch_i8_merge<1>(gp, rows, norms, n, dim, d_q, nq, (int)metric, (int)kc, lists, proof, fa, st); break;
+            case 2: launch_i8_merge<2>(gp, rows, norms, n, dim, d_q, nq, (int)metric, (int)kc, lists, proof, fa, st); break;
+            case 3: launch_i8_merge<3>(gp, rows, norms, n, dim, d_q, nq, (int)metric, (int)kc, lists, proof, fa, st); break;
+            case 4: launch_i8_merge<4>(gp, rows, norms, n, dim, d_q, nq, (int)metric, (int)kc, lists, proof, fa, st); break;
+            case 6: launch_i8_merge<6>(gp, rows, norms, n, dim, d_q, nq, (int)metric, (int)kc, lists, proof, fa, st); break;
+            case 8: launch_i8_merge<8>(gp, rows, norms, n, dim, d_q, nq, (int)metric, (int)kc, lists, proof, fa, st); break;
+            default: return fail(MANS_PIPELINE_UNAVAILABLE, "int8 scan: unsupported dim");
+            }
+            e = hipGetLastError();
+        }
+        ctx->time_end(slot, st, "int8_merge");
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(slot->status_h.p, slot->status.p, (size_t)nq, hipMemcpyDeviceToHost, st);
+        if (e == hipSuccess) e = hipStreamSynchronize(st);
+        if (e != hipSuccess) return hip_fail(e, "int8 batch scan");
+        std::vector<uint32_t> redo;
+        const uint8_t* sh = (const uint8_t*)slot->status_h.p;
+        for (int64_t i = 0; i < nq; ++i) {
+            if (sh[i] == kStatusReselect) {
+                redo.push_back((uint32_t)i);
+                continue;
+            }
+            rounds[i] += 1;
+            if (sh[i]) grow.push_back((uint32_t)i);
+        }
+        ctx->reselects += (int64_t)redo.size();
+        if (!redo.empty()) {
+            int rc = stream_round(redo, kc, true, grow);
+            if (rc != MANS_OK) return rc;
+            std::sort(grow.begin(), grow.end());
+        }
+        return MANS_OK;
+    };
+
     std::vector<uint32_t> pending;  // empty = all queries
-    int64_t npend = nq;
     bool first = true;
     for (;;) {
         if (kc > kInt8MaxBudget) {
@@ -443,68 +903,18 @@ static int int8_search_run(mans_ctx* ctx, mans_corpus* c, const float* d_q, int6
             for (uint32_t qi : *idx) rounds[qi] += 1;
             return finish(int8_exact_fallback(ctx, c, d_q, *idx, k, metric, d_dist, d_ids, st, slot));
         }
-        static const int64_t target = [] {
-            const char* e = std::getenv("MANS_INT8_BLOCKS");
-            return e ? std::max<int64_t>(1, std::atoll(e)) : (int64_t)512;
-        }();
-        FlatPlan p = plan_flat(n, npend, (int)kc, target);
-        const uint32_t* d_qidx = nullptr;
-        if (!pending.empty()) {
-            e = slot->qidx.ensure(pending.size() * sizeof(uint32_t), ctx->fail_alloc);
-            if (e == hipSuccess)
-                e = hipMemcpyAsync(slot->qidx.p, pending.data(), pending.size() * sizeof(uint32_t),
-                                   hipMemcpyHostToDevice, st);
-            d_qidx = (const uint32_t*)slot->qidx.p;
-        }
-        FlatBuffers fb;
-        if (e == hipSuccess) e = prepare_flat_buffers(ctx, slot, p, npend, st, &fb);
-        if (e == hipSuccess) e = slot->status_h.ensure((size_t)npend);
-        if (e != hipSuccess) return hip_fail(e, "int8 scan workspace");
-        FlatArgs fa = {};
-        fa.cand = fb.cand;
-        fa.gcand = fb.gcand;
-        fa.counters = fb.counters;
-        fa.out_dist = d_dist;
-        fa.out_ids = d_ids;
-        fa.status = fb.status;
-        fa.k = keff;
-        fa.k_stride = (int)k;
-        fa.group_blocks = p.group_blocks;
-        fa.ngroups = p.ngroups;
-        const int proof = mode == 0 ? kProofMargin : kProofNone;
-        if (!first) ctx->time_begin(slot, st);
-        switch (nch) {
-        case 1: launch_int8_scan<1>(p, pl, (const float*)c->rows.p, (const float*)c->norms.p, n, dim, d_q, d_qidx, npend, qcodes, coefs, (int)metric, proof, fa, st); break;
-        case 2: launch_int8_scan<2>(p, pl, (const float*)c->rows.p, (const float*)c->norms.p, n, dim, d_q, d_qidx, npend, qcodes, coefs, (int)metric, proof, fa, st); break;
-        case 3: launch_int8_scan<3>(p, pl, (const float*)c->rows.p, (const float*)c->norms.p, n, dim, d_q, d_qidx, npend, qcodes, coefs, (int)metric, proof, fa, st); break;
-        case 4: launch_int8_scan<4>(p, pl, (const float*)c->rows.p, (const float*)c->norms.p, n, dim, d_q, d_qidx, npend, qcodes, coefs, (int)metric, proof, fa, st); break;
-        case 6: launch_int8_scan<6>(p, pl, (const float*)c->rows.p, (const float*)c->norms.p, n, dim, d_q, d_qidx, npend, qcodes, coefs, (int)metric, proof, fa, st); break;
-        case 8: launch_int8_scan<8>(p, pl, (const float*)c->rows.p, (const float*)c->norms.p, n, dim, d_q, d_qidx, npend, qcodes, coefs, (int)metric, proof, fa, st); break;
-        default: return fail(MANS_PIPELINE_UNAVAILABLE, "int8 scan: unsupported dim");
-        }
-        e = hipGetLastError();
-        ctx->time_end(slot, st, "int8_scan");
-        first = false;
-        if (e == hipSuccess)
-            e = hipMemcpyAsync(slot->status_h.p, fb.status, (size_t)npend, hipMemcpyDeviceToHost, st);
-        if (e == hipSuccess) e = hipStreamSynchronize(st);
-        if (e != hipSuccess) {
-            slot->counters_dirty = true;
-            return hip_fail(e, "int8 scan");
-        }
-        const uint8_t* sh = (const uint8_t*)slot->status_h.p;
         std::vector<uint32_t> next;
-        for (int64_t i = 0; i < npend; ++i) {
-            const uint32_t qi = pending.empty() ? (uint32_t)i : pending[i];
-            rounds[qi] += 1;
-            if (sh[i]) next.push_back(qi);
-        }
+        I8GemmPlan gp;
+        int rc;
+        if (first && plan_i8gemm(n, stride, nq, kc, &gp)) rc = gemm_round(gp, kc, next);
+        else rc = stream_round(pending, kc, !first, next);
+        if (rc != MANS_OK) return rc;
+        first = false;
         if (next.empty()) return finish(MANS_OK);
         if (kc >= n) return fail(MANS_SEARCH_FAILED, "int8 scan: proof failed with every row selected");
         pending.swap(next);
-        npend = (int64_t)pending.size();
         kc = std::min<int64_t>(kc * 4, n);
-        ctx->proof_retries += npend;
+        ctx->proof_retries += (int64_t)pending.size();
     }
 }
 

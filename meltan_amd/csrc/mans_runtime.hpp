@@ -69,6 +69,7 @@ struct mans_ctx {
     std::vector<mans::Slot*> all_slots;
     std::atomic<bool> timing{false};
     std::atomic<int64_t> proof_retries{0};
+    std::atomic<int64_t> reselects{0};  // batched int8 queries selected again by the streaming scan
     std::mutex tmu;
     std::map<std::string, std::pair<double, int64_t>> times;
 

@@ -433,18 +433,29 @@ enum ProofMode : int {
     kProofNone = 2,    // fixed budget: no proof (status 0)
 };
 
+// Status of a query after a launch: 0 done, 1 proof failed (grow the
+// candidate count), kStatusReselect: the bounded lists could not show that
+// the candidates are the kc smallest keys (select again at the same kc with
+// the streaming scan).
+constexpr uint8_t kStatusReselect = 2;
+
 // The last block of a query: exact rescore of the kc candidates held in
 // lds[0, kc), sort by (distance, id), outputs and proof status.  qv: the
 // query chunks.  lds must hold kc + pow2(kc) slots (cap >= 2 kc, 4 caps).
 // Candidate ids index `rows`; idmap (nullable) maps them to the ids that are
 // reported and that order ties.  n: the number of rows the query could see.
 // status_idx: the status slot (default: blockIdx.y).
+// sel_cut: the smallest largest slot over bounded lists that turned rows
+// away (kEmptySlot: none did).  Such a row's slot is above sel_cut, so the
+// candidates are the exact kc smallest slots only when the kc-th is <=
+// sel_cut; otherwise the status is kStatusReselect and nothing else holds.
 template <int NCH>
 __device__ __forceinline__ void final_rescore_f4(const f4v* qv, const float* __restrict__ rows,
                                  const float* __restrict__ norms, int64_t n, int dim, int metric,
                                  uint32_t q, uint64_t* lds, int kc, const FlatArgs& fa,
                                  float list_cut = kFltMax, int proof = kProofFlat,
-                                 const uint32_t* idmap = nullptr, int status_idx = -1) {
+                                 const uint32_t* idmap = nullptr, int status_idx = -1,
+                                 uint64_t sel_cut = kEmptySlot) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int grp = lane >> 4, lr = lane & 15, dim4 = dim >> 2;
     __shared__ int ncand_sh;
@@ -514,7 +525,9 @@ __device__ __forceinline__ void final_rescore_f4(const f4v* qv, const float* __r
         } else {
             ok = all_rows || (kout > 0 && cutoff >= slot_key(res[kout - 1]));
         }
-        fa.status[status_idx >= 0 ? status_idx : (int)blockIdx.y] = ok ? 0 : 1;
+        const bool sel_exact = sel_cut == kEmptySlot || (ncand == kc && top[kc - 1] <= sel_cut);
+        fa.status[status_idx >= 0 ? status_idx : (int)blockIdx.y] =
+            !sel_exact ? kStatusReselect : (ok ? 0 : 1);
     }
 }
 
