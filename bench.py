@@ -273,7 +273,7 @@ def bench_int8(args, ctx):
             corpus.int8_search_device(dq.offset(off * dim), b, k, metric, 1, budget,
                                       dd.offset(off * k), di.offset(off * k), stream.handle)
         elapsed = timed(step, steps, 2, hip)
-        kt = kernel_avg(ctx, step, min(steps, 10), ["int8_scan", "int8_gemm", "int8_merge"], hip)
+        kt = kernel_avg(ctx, step, min(steps, 10), ["int8_scan", "int8_bound", "int8_gemm", "int8_merge"], hip)
         if b == 1:
             avg, launches = kt["int8_scan"]
             per = b * min(steps, 10) // max(launches, 1)
@@ -286,8 +286,9 @@ def bench_int8(args, ctx):
             roof = {"bound": "mfma", "achieved": round(ops / avg / 1e12, 2), "peak": 5000.0,
                     "unit": "TOP/s", "frac": round(ops / avg / 1e12 / 5000.0, 5),
                     "traffic": measured_traffic("int8_gemm<12>", f"int8_{n}x{dim}_b{b}"),
-                    "kernel": "int8_gemm<12,cosine>", "avg_launch_us": round(avg * 1e6, 2),
+                    "kernel": "int8_gemm<12,cosine,bounded>", "avg_launch_us": round(avg * 1e6, 2),
                     "ops_per_launch": int(ops),
+                    "bound_pass_us": round(kt["int8_bound"][0] * 1e6, 2) if kt["int8_bound"][1] else None,
                     "merge_avg_us": round(kt["int8_merge"][0] * 1e6, 2) if kt["int8_merge"][1] else None,
                     "reselect_scan_launches": kt["int8_scan"][1]}
         out[f"batch{b}"] = {"qps": round(b * steps / elapsed, 1), "roofline": roof}

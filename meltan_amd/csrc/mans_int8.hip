@@ -313,6 +313,13 @@ static void launch_int8_scan(const FlatPlan& p, const Int8Planes& pl, const floa
 // first rows is rare.  A stage's keys are offered while the next stage's
 // MFMAs run.
 //
+// A first launch over the first sixteenth of every segment gives each
+// query a bound: the kc-th smallest slot of its sampled lists, above which
+// no slot can be among the query's kc smallest over all rows (kc sampled
+// rows are at or below it).  The full launch then lets a key in only when
+// it is at most the bound and beats the lane's largest slot, which keeps
+// insertions into the lane lists rare.
+//
 // int8_lists_merge then selects each query's kc smallest slots over its
 // 2 nseg lists.  A row a full list turned away has a slot above that list's
 // largest, so the selection equals the streaming scan's (the kc smallest
@@ -325,10 +332,12 @@ constexpr int kI8List = 8;       // slots per lane list
 constexpr int kI8GemmMaxKc = 256;
 
 struct I8GemmArgs {
-    int nseg;              // row segments (multiple of 8)
-    int nqb;               // query blocks
-    int64_t rows_per_seg;  // multiple of kI8Rows
-    uint64_t* lists;       // [nq][nseg][2][kI8List]
+    int nseg;                 // row segments (multiple of 8)
+    int nqb;                  // query blocks
+    int64_t rows_per_seg;     // multiple of kI8Rows
+    int64_t seg_rows;         // rows scanned from each segment's start (<= rows_per_seg)
+    const uint64_t* qbound;   // nullable, per query: no slot above it is ever needed
+    uint64_t* lists;          // [nq][nseg][2][kI8List]
 };
 
 // KS 32-byte k-steps per row: the code stride is 32 KS or 32 KS - 16 (the
@@ -364,7 +373,8 @@ __device__ __forceinline__ void lane_list_insert(uint64_t (&l)[C], uint64_t s) {
 // 8 (b / (8 nqb)) + b % 8 and query block (b % (8 nqb)) / 8: the query
 // blocks of one segment share b % 8, which places them on one XCD, so the
 // segment's codes are read from HBM once into that XCD's L2.
-template <int KS, int METRIC>
+// BOUNDED: the full launch (per-query bounds); otherwise the sampled one.
+template <int KS, int METRIC, bool BOUNDED>
 __global__ __launch_bounds__(256) void int8_gemm(Int8Planes pl, int64_t n,
                                                  const int8_t* __restrict__ qcodes,
                                                  const Int8QueryCoef* __restrict__ coefs, int64_t nq,
@@ -399,9 +409,14 @@ __global__ __launch_bounds__(256) void int8_gemm(Int8Planes pl, int64_t n,
     uint64_t lst[C];
 #pragma unroll
     for (int i = 0; i < C; ++i) lst[i] = kEmptySlot;
+    // Slots above `bound` never enter; keys above thr (the key of the
+    // smaller of bound and the lane's largest slot) cannot pass.
+    const uint64_t bound = !qvalid ? 0ull : (BOUNDED ? ga.qbound[qid] : kEmptySlot);
+    float thr = !qvalid ? -__int_as_float(0x7F800000)
+                        : (bound == kEmptySlot ? __int_as_float(0x7F800000) : slot_key(bound));
 
     const int64_t seg0 = (int64_t)seg * ga.rows_per_seg;
-    const int64_t seg1 = seg0 + ga.rows_per_seg < n ? seg0 + ga.rows_per_seg : n;
+    const int64_t seg1 = seg0 + ga.seg_rows < n ? seg0 + ga.seg_rows : n;
     const int64_t nst = seg1 > seg0 ? (seg1 - seg0 + kI8Rows - 1) / kI8Rows : 0;
 
     // The LDS pad chunk of each row (a stride of 32 KS - 16) stays zero.
@@ -422,8 +437,8 @@ __global__ __launch_bounds__(256) void int8_gemm(Int8Planes pl, int64_t n,
             int64_t row = seg0 + st * kI8Rows + r;
             row = row < seg1 ? row : seg1 - 1;
             const int cc = c < row_chunks ? c : row_chunks - 1;
-            pre[u] = __builtin_nontemporal_load(
-                reinterpret_cast<const i4v*>(pl.codes + row * stride + 16 * cc));
+            // Plain loads: the eight query blocks of a segment share it in L2.
+            pre[u] = *reinterpret_cast<const i4v*>(pl.codes + row * stride + 16 * cc);
         }
     };
     auto store_stage = [&](int buf) {
@@ -435,31 +450,60 @@ __global__ __launch_bounds__(256) void int8_gemm(Int8Planes pl, int64_t n,
                 *reinterpret_cast<i4v*>(xs + buf * G::STAGE + r * G::RS + 16 * c) = pre[u];
         }
     };
-    auto store_coef = [&](int64_t st) {
+    // Rows past the segment's end get NaN coefficients: their keys are NaN
+    // and never pass the threshold test.  cb: the stage's coefficient buffer.
+    auto store_coef = [&](int64_t st, int cb) {
         if (tid < kI8Rows) {
-            int64_t row = seg0 + st * kI8Rows + tid;
-            row = row < seg1 ? row : seg1 - 1;
-            float* c = cf + (int)(st % 3) * 3 * kI8Rows;
-            c[tid] = pl.u[row];
-            c[kI8Rows + tid] = pl.w[row];
-            c[2 * kI8Rows + tid] = METRIC == kMetricL2 ? pl.normsq[row] : pl.invsqrt[row];
+            const int64_t row = seg0 + st * kI8Rows + tid;
+            const bool in = row < seg1;
+            const int64_t r = in ? row : seg1 - 1;
+            const float nan = __int_as_float(0x7FC00000);
+            float* c = cf + cb * 3 * kI8Rows;
+            c[tid] = in ? pl.u[r] : nan;
+            c[kI8Rows + tid] = in ? pl.w[r] : nan;
+            c[2 * kI8Rows + tid] = in ? (METRIC == kMetricL2 ? pl.normsq[r] : pl.invsqrt[r]) : nan;
         }
     };
-    // Offers stage st's 32 keys per lane (st < 0: nothing).
-    auto offer = [&](const i16v& a0, const i16v& a1, int64_t st) {
+    // Offers stage st's 32 keys per lane (st < 0: nothing).  All keys are
+    // computed first, branch-free; only a lane whose smallest key is at or
+    // below thr takes the insertion path, where each slot is checked
+    // exactly.
+    auto offer = [&](const i16v& a0, const i16v& a1, int64_t st, int cb) {
         if (st < 0) return;
-        const float* c = cf + (int)(st % 3) * 3 * kI8Rows;
+        const float* c = cf + cb * 3 * kI8Rows;
+        float key[32];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int m = 32 * t + 8 * (v >> 2) + 4 * h + (v & 3);
-                const int64_t row = seg0 + st * kI8Rows + m;
-                const float dot = (float)(t == 0 ? a0[v] : a1[v]);
-                const float pn = c[2 * kI8Rows + m];
-                const float key = int8_key(METRIC, coef, dot, c[m], c[kI8Rows + m], pn, pn);
-                const uint64_t s = (qvalid && row < seg1) ? pack_slot(key, (uint32_t)row) : kEmptySlot;
-                if (s < lst[C - 1]) lane_list_insert<C>(lst, s);
+            for (int g = 0; g < 4; ++g) {
+                const int m0 = 32 * t + 8 * g + 4 * h;  // four consecutive rows
+                const f4v cu = *reinterpret_cast<const f4v*>(c + m0);
+                const f4v cw = *reinterpret_cast<const f4v*>(c + kI8Rows + m0);
+                const f4v cn = *reinterpret_cast<const f4v*>(c + 2 * kI8Rows + m0);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int v = 4 * g + j;
+                    const float dot = (float)(t == 0 ? a0[v] : a1[v]);
+                    key[16 * t + v] = int8_key(METRIC, coef, dot, cu[j], cw[j], cn[j], cn[j]);
+                }
+            }
+        }
+        float mn = key[0];
+#pragma unroll
+        for (int i = 1; i < 32; ++i) mn = fminf(mn, key[i]);  // NaN keys drop out
+        if (mn <= thr) {
+            const int64_t base = seg0 + st * kI8Rows;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                if (key[i] <= thr) {
+                    const int m = 32 * (i >> 4) + 8 * ((i & 15) >> 2) + 4 * h + (i & 3);
+                    const uint64_t slot = pack_slot(key[i], (uint32_t)(base + m));
+                    if (slot <= bound) {
+                        lane_list_insert<C>(lst, slot);
+                        const uint64_t top = lst[C - 1] < bound ? lst[C - 1] : bound;
+                        thr = top == kEmptySlot ? thr : slot_key(top);
+                    }
+                }
             }
         }
     };
@@ -467,10 +511,11 @@ __global__ __launch_bounds__(256) void int8_gemm(Int8Planes pl, int64_t n,
     if (nst > 0) {
         load_stage(0);
         store_stage(0);
-        store_coef(0);
+        store_coef(0, 0);
     }
     __syncthreads();
     int buf = 0;
+    int cb = 0;  // st % 3
     i16v prev0 = {}, prev1 = {};
     for (int64_t st = 0; st < nst; ++st) {
         // Prefetch the next stage (past the last one, reload the last).
@@ -485,18 +530,20 @@ __global__ __launch_bounds__(256) void int8_gemm(Int8Planes pl, int64_t n,
             acc0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, qreg[s], acc0, 0, 0, 0);
             acc1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, qreg[s], acc1, 0, 0, 0);
         }
+        const int cb_prev = cb == 0 ? 2 : cb - 1, cb_next = cb == 2 ? 0 : cb + 1;
         // The previous stage's keys, while this stage's MFMAs run.
-        offer(prev0, prev1, st - 1);
+        offer(prev0, prev1, st - 1, cb_prev);
         if (st + 1 < nst) {
             store_stage(buf ^ 1);  // last read before the previous barrier
-            store_coef(st + 1);
+            store_coef(st + 1, cb_next);
         }
         __syncthreads();
         buf ^= 1;
+        cb = cb_next;
         prev0 = acc0;
         prev1 = acc1;
     }
-    offer(prev0, prev1, nst - 1);
+    offer(prev0, prev1, nst - 1, cb == 0 ? 2 : cb - 1);
     if (qvalid) {
         uint64_t* out = ga.lists + (((size_t)qid * ga.nseg + seg) * 2 + h) * C;
 #pragma unroll
@@ -540,6 +587,19 @@ __global__ __launch_bounds__(256) void int8_lists_merge(
                           -1, (uint64_t)cut);
 }
 
+// grid (1, nq): each query's bound, the kc-th smallest slot of its lists
+// from the sampled launch (kEmptySlot when they hold fewer than kc).
+__global__ __launch_bounds__(256) void int8_lists_bound(int kc, int cap, int nlists,
+                                                        const uint64_t* __restrict__ lists,
+                                                        uint64_t* __restrict__ qbound) {
+    extern __shared__ uint64_t lds[];
+    const uint32_t q = blockIdx.y;
+    WaveTopK sel;
+    block_select_lists(lists + (size_t)q * nlists * kI8List, (int64_t)nlists * kI8List, lds, cap,
+                       kc, sel);  // ends in a barrier
+    if (threadIdx.x == 0) qbound[q] = lds[kc - 1];
+}
+
 static bool i8gemm_ks(int stride, int* ks) {
     const int k = (stride + 31) / 32;
     switch (k) {
@@ -553,6 +613,11 @@ struct I8GemmPlan {
     int nseg = 0;
     int nqb = 0;
     int64_t rows_per_seg = 0;
+    // The bounding launch: s_nseg segments of s_rows_per_seg rows, the
+    // first s_seg_rows of each scanned (about a sixteenth of the rows).
+    int s_nseg = 0;
+    int64_t s_rows_per_seg = 0;
+    int64_t s_seg_rows = 0;
 };
 
 static bool plan_i8gemm(int64_t n, int stride, int64_t nq, int64_t kc, I8GemmPlan* out) {
@@ -576,6 +641,14 @@ static bool plan_i8gemm(int64_t n, int stride, int64_t nq, int64_t kc, I8GemmPla
     const int64_t rps = (n + nseg - 1) / nseg;
     p.rows_per_seg = (rps + kI8Rows - 1) / kI8Rows * kI8Rows;
     p.nseg = (int)nseg;
+    // Fewer, longer sampled segments than the full launch: each lane list
+    // then sees enough rows to settle, and the bound selects over fewer lists.
+    p.s_nseg = (int)std::min<int64_t>(nseg, 64);
+    const int64_t srps = (n + p.s_nseg - 1) / p.s_nseg;
+    p.s_rows_per_seg = (srps + kI8Rows - 1) / kI8Rows * kI8Rows;
+    int64_t srows = (n / 16 / p.s_nseg + kI8Rows - 1) / kI8Rows * kI8Rows;
+    srows = std::max<int64_t>(srows, kI8Rows);
+    p.s_seg_rows = std::min(srows, p.s_rows_per_seg);
     *out = p;
     return true;
 }
@@ -584,31 +657,35 @@ template <int KS>
 static void launch_i8gemm_ks(const I8GemmPlan& p, const Int8Planes& pl, int64_t n,
                              const int8_t* qcodes, const Int8QueryCoef* coefs, int64_t nq,
                              int metric, const I8GemmArgs& ga, hipStream_t s) {
-    const dim3 grid((unsigned)(p.nseg * p.nqb));
+    const dim3 grid((unsigned)(ga.nseg * p.nqb));
     const size_t shmem = i8gemm_lds_bytes<KS>();
+    const bool b = ga.qbound != nullptr;
     switch (metric) {
     case kMetricCosine:
-        hipLaunchKernelGGL((int8_gemm<KS, kMetricCosine>), grid, dim3(256), shmem, s, pl, n, qcodes,
-                           coefs, nq, ga);
+        if (b) hipLaunchKernelGGL((int8_gemm<KS, kMetricCosine, true>), grid, dim3(256), shmem, s, pl, n, qcodes, coefs, nq, ga);
+        else hipLaunchKernelGGL((int8_gemm<KS, kMetricCosine, false>), grid, dim3(256), shmem, s, pl, n, qcodes, coefs, nq, ga);
         break;
     case kMetricL2:
-        hipLaunchKernelGGL((int8_gemm<KS, kMetricL2>), grid, dim3(256), shmem, s, pl, n, qcodes,
-                           coefs, nq, ga);
+        if (b) hipLaunchKernelGGL((int8_gemm<KS, kMetricL2, true>), grid, dim3(256), shmem, s, pl, n, qcodes, coefs, nq, ga);
+        else hipLaunchKernelGGL((int8_gemm<KS, kMetricL2, false>), grid, dim3(256), shmem, s, pl, n, qcodes, coefs, nq, ga);
         break;
     default:
-        hipLaunchKernelGGL((int8_gemm<KS, kMetricIP>), grid, dim3(256), shmem, s, pl, n, qcodes,
-                           coefs, nq, ga);
+        if (b) hipLaunchKernelGGL((int8_gemm<KS, kMetricIP, true>), grid, dim3(256), shmem, s, pl, n, qcodes, coefs, nq, ga);
+        else hipLaunchKernelGGL((int8_gemm<KS, kMetricIP, false>), grid, dim3(256), shmem, s, pl, n, qcodes, coefs, nq, ga);
         break;
     }
 }
 
 static hipError_t launch_i8gemm(const I8GemmPlan& p, const Int8Planes& pl, int64_t n,
                                 const int8_t* qcodes, const Int8QueryCoef* coefs, int64_t nq,
-                                int metric, uint64_t* lists, hipStream_t s) {
+                                int metric, bool sampled, const uint64_t* qbound,
+                                uint64_t* lists, hipStream_t s) {
     I8GemmArgs ga;
-    ga.nseg = p.nseg;
+    ga.nseg = sampled ? p.s_nseg : p.nseg;
     ga.nqb = p.nqb;
-    ga.rows_per_seg = p.rows_per_seg;
+    ga.rows_per_seg = sampled ? p.s_rows_per_seg : p.rows_per_seg;
+    ga.seg_rows = sampled ? p.s_seg_rows : p.rows_per_seg;
+    ga.qbound = qbound;
     ga.lists = lists;
     switch (p.ks) {
     case 2: launch_i8gemm_ks<2>(p, pl, n, qcodes, coefs, nq, metric, ga, s); break;
@@ -836,13 +913,27 @@ static int int8_search_run(mans_ctx* ctx, mans_corpus* c, const float* d_q, int6
     // show an exact selection repeat the round on the streaming scan.
     auto gemm_round = [&](const I8GemmPlan& gp, int64_t kc, std::vector<uint32_t>& grow) -> int {
         const size_t lbytes = (size_t)nq * gp.nseg * 2 * kI8List * sizeof(uint64_t);
-        hipError_t e = slot->cand.ensure(lbytes, ctx->fail_alloc);
+        hipError_t e = slot->cand.ensure(lbytes + (size_t)nq * sizeof(uint64_t), ctx->fail_alloc);
         if (e == hipSuccess) e = slot->status.ensure((size_t)nq, ctx->fail_alloc);
         if (e == hipSuccess) e = slot->status_h.ensure((size_t)nq);
         if (e != hipSuccess) return hip_fail(e, "int8 batch workspace");
         uint64_t* lists = (uint64_t*)slot->cand.p;
+        uint64_t* qbound = lists + lbytes / sizeof(uint64_t);
+        // Bounds from the sampled rows, then the full contraction.
         ctx->time_begin(slot, st);
-        e = launch_i8gemm(gp, pl, n, qcodes, coefs, nq, (int)metric, lists, st);
+        e = launch_i8gemm(gp, pl, n, qcodes, coefs, nq, (int)metric, true, nullptr, lists, st);
+        if (e == hipSuccess) {
+            const int bcap = flat_cap_for((int)kc);
+            hipLaunchKernelGGL(int8_lists_bound, dim3(1, (unsigned)nq), dim3(256),
+                               sizeof(uint64_t) * 4 * (size_t)bcap, st, (int)kc, bcap, 2 * gp.s_nseg,
+                               (const uint64_t*)lists, qbound);
+            e = hipGetLastError();
+        }
+        ctx->time_end(slot, st, "int8_bound");
+        ctx->time_begin(slot, st);
+        if (e == hipSuccess)
+            e = launch_i8gemm(gp, pl, n, qcodes, coefs, nq, (int)metric, false, qbound,
+                              lists, st);
         ctx->time_end(slot, st, "int8_gemm");
         FlatArgs fa = {};
         fa.out_dist = d_dist;
