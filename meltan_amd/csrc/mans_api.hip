@@ -230,6 +230,7 @@ int mans_corpus_write_rows(mans_corpus* c, int64_t first_row, const float* rows,
         e = launch_row_norms(dst, count, (int)c->dim, (float*)c->norms.p + first_row, nullptr);
     if (e == hipSuccess && c->int8_valid)
         e = int8_refresh_rows(c, first_row, count, nullptr);
+    c->bf_valid = false;  // the split parts are rebuilt on next use
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) return hip_fail(e, "corpus write");
     return MANS_OK;
@@ -239,6 +240,7 @@ int mans_corpus_invalidate(mans_corpus* c) {
     if (!c) return fail(MANS_SEARCH_FAILED, "mans_corpus_invalidate: NULL");
     std::lock_guard<std::mutex> g(c->mu);
     c->int8_valid = false;
+    c->bf_valid = false;
     return MANS_OK;
 }
 
@@ -353,6 +355,41 @@ hipError_t stage_from_device(Slot* s, void* dst0, const void* src0, size_t b0, v
 // Runs the flat scan for queries already in device memory.  The proof loop
 // (kc x4 per round, exact keys past kc = 1024) mirrors the budget growth of
 // BoundedExactScan.swift:96-121.
+// MANS_BF3=0 keeps batches on the fp32 contraction.
+static bool bf3_enabled() {
+    static const bool on = [] {
+        const char* e = std::getenv("MANS_BF3");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+
+// Builds the split-bf16 parts of the rows on first use (and after writes).
+static int bf16_split_ensure(mans_ctx* ctx, const mans_corpus* cc, hipStream_t st) {
+    mans_corpus* c = const_cast<mans_corpus*>(cc);
+    std::lock_guard<std::mutex> g(c->mu);
+    if (c->bf_valid) return MANS_OK;
+    if (c->dim % 16 != 0) {
+        c->bf_valid = true;
+        c->bf_ok = false;
+        return MANS_OK;
+    }
+    hipError_t e = c->bf_split.ensure((size_t)c->n * c->dim * sizeof(uint32_t), ctx->fail_alloc);
+    if (e == hipSuccess) e = c->bf_flag.ensure(sizeof(uint32_t), ctx->fail_alloc);
+    if (e == hipSuccess) e = hipMemsetAsync(c->bf_flag.p, 0, sizeof(uint32_t), st);
+    if (e == hipSuccess)
+        e = launch_split_bf16((const float*)c->rows.p, c->n, (int)c->dim, (uint32_t*)c->bf_split.p,
+                              (uint32_t*)c->bf_flag.p, false, st);
+    uint32_t flag = 1;
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(&flag, c->bf_flag.p, sizeof(uint32_t), hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) return hip_fail(e, "split-bf16 rows");
+    c->bf_valid = true;
+    c->bf_ok = flag == 0;
+    return MANS_OK;
+}
+
 static int flat_search_chunk(mans_ctx* ctx, const mans_corpus* c, const float* d_q, int64_t nq,
                              int64_t k, uint32_t metric, float* d_dist, uint32_t* d_ids,
                              hipStream_t st, Slot* slot, float* h_dist, uint32_t* h_ids);
@@ -403,24 +440,53 @@ static int flat_search_chunk(mans_ctx* ctx, const mans_corpus* c, const float* d
         hipError_t e = hipSuccess;
         GemmPlan gp;
         if (pending.empty() && !exact && plan_gemm(n, dim, npend, kc, &gp)) {
-            // First round of a batch: MFMA contraction + per-query merge.
-            e = slot->cand.ensure(gemm_lists_bytes(gp, npend), ctx->fail_alloc);
+            // First round of a batch: MFMA contraction + per-query merge,
+            // on split-bf16 MFMA when the corpus allows it, else fp32 MFMA.
+            const bool bf3 = bf3_enabled() && bf16_split_ensure(ctx, c, st) == MANS_OK && c->bf_ok;
+            const size_t lbytes = gemm_lists_bytes(gp, npend);
+            e = slot->cand.ensure(lbytes + (size_t)npend * sizeof(uint64_t), ctx->fail_alloc);
             if (e == hipSuccess) e = slot->status.ensure((size_t)npend, ctx->fail_alloc);
             if (e == hipSuccess) e = slot->status_h.ensure((size_t)npend);
+            if (e == hipSuccess && bf3)
+                e = slot->qsplit.ensure((size_t)npend * dim * sizeof(uint32_t), ctx->fail_alloc);
+            if (e == hipSuccess && bf3)
+                e = slot->qbad.ensure((size_t)npend * sizeof(uint32_t), ctx->fail_alloc);
             if (e != hipSuccess) return hip_fail(e, "flat scan workspace");
             FlatBuffers fb;
             fb.out_dist = d_dist;
             fb.out_ids = d_ids;
             fb.status = (uint8_t*)slot->status.p;
-            ctx->time_begin(slot, st);
-            e = launch_flat_gemm(gp, (const float*)c->rows.p, (const float*)c->norms.p, n, dim, d_q,
-                                 npend, (int)metric, (uint64_t*)slot->cand.p, st);
-            ctx->time_end(slot, st, "flat_gemm");
+            uint64_t* lists = (uint64_t*)slot->cand.p;
+            uint64_t* qbound = bf3 ? lists + lbytes / sizeof(uint64_t) : nullptr;
+            const uint32_t* qbad = bf3 ? (const uint32_t*)slot->qbad.p : nullptr;
+            const float* rows = (const float*)c->rows.p;
+            const float* norms = (const float*)c->norms.p;
+            if (bf3) {
+                uint32_t* qs = (uint32_t*)slot->qsplit.p;
+                const uint32_t* rs = (const uint32_t*)c->bf_split.p;
+                ctx->time_begin(slot, st);
+                e = hipMemsetAsync(slot->qbad.p, 0, (size_t)npend * sizeof(uint32_t), st);
+                if (e == hipSuccess)
+                    e = launch_split_bf16(d_q, npend, dim, qs, (uint32_t*)slot->qbad.p, true, st);
+                if (e == hipSuccess)
+                    e = launch_flat_bf3(gp, true, rs, norms, n, dim, qs, d_q, npend, (int)metric,
+                                        nullptr, lists, st);
+                if (e == hipSuccess) e = launch_bf3_bounds(gp, npend, lists, qbound, st);
+                ctx->time_end(slot, st, "flat_bound");
+                ctx->time_begin(slot, st);
+                if (e == hipSuccess)
+                    e = launch_flat_bf3(gp, false, rs, norms, n, dim, qs, d_q, npend, (int)metric,
+                                        qbound, lists, st);
+                ctx->time_end(slot, st, "flat_gemm");
+            } else {
+                ctx->time_begin(slot, st);
+                e = launch_flat_gemm(gp, rows, norms, n, dim, d_q, npend, (int)metric, lists, st);
+                ctx->time_end(slot, st, "flat_gemm");
+            }
             ctx->time_begin(slot, st);
             if (e == hipSuccess)
-                e = launch_flat_gemm_merge(gp, (const float*)c->rows.p, (const float*)c->norms.p, n,
-                                           dim, d_q, npend, (int)metric,
-                                           (const uint64_t*)slot->cand.p, fb, keff, kstride, st);
+                e = launch_flat_gemm_merge(gp, rows, norms, n, dim, d_q, npend, (int)metric, lists,
+                                           qbound, qbad, fb, keff, kstride, st);
             ctx->time_end(slot, st, "flat_merge");
         } else {
             FlatPlan p = plan_flat(n, npend, kc);

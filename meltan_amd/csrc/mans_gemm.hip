@@ -250,13 +250,322 @@ __global__ __launch_bounds__(256) void flat_gemm_f32(
     }
 }
 
+// ---------------------------------------------------------------------------
+// Batched queries on bf16 MFMA with fp32-level accuracy (split products).
+//
+// Every value x in [2^-50, 2^50] (or 0) is split once into bf16 parts
+// x = xh + xl + r: xh = bf16(x), xl = bf16(x - xh) (x - xh is exact in
+// fp32), both rounded to nearest even, so |x - xh| <= 2^-8 |x| and
+// |r| <= 2^-16 |x|.  The contraction sums qh vh, qh vl and ql vh with
+// v_mfma_f32_32x32x16_bf16 into three fp32 accumulators (each product of
+// two bf16 values is exact in fp32), combined as hh + (hl + lh).  The
+// omitted terms ql vl + (qh + ql) rv + rq (vh + vl) + rq rv are at most
+// 3.01 2^-16 |q_i v_i| per element, the accumulations add at most
+// gamma_d (u = 2^-23) (1 + 2^-7 + 2^-7) sum |q_i v_i| and the two final
+// additions 2^-22 of it, so
+//   |f - q.v| <= g sum |q_i v_i|,  g = 1.024 gamma_d + 3.01 2^-16 + 2^-22,
+// and the keys are the fp32 path's lower bounds computed with a unit
+// roundoff u_eff for which gamma_d(u_eff) = g (>= every other error term
+// those bounds cover).  Values outside the range (huge, tiny, inf, NaN)
+// are flagged when split: a corpus with any such value keeps the fp32
+// contraction, and a flagged query is re-run by the streaming scan.
+//
+// The split parts are stored per 8 elements as [8 hi | 8 lo] (32 bytes),
+// so a row keeps its fp32 size and one 16-element MFMA step of a lane is
+// two 16-byte reads.
+//
+// The epilogue admits a key only when it is at or below the lane's
+// threshold (its largest slot, or the query's bound): a first launch over
+// a sample of rows (the first rows of 64 spread segments) gives each query
+// its bound, the kc-th smallest slot of the sampled lists; no slot above it
+// is among the query's kc smallest, and the merge's proof cutoff takes it
+// into account.
+
+__device__ __forceinline__ uint32_t bf16_rne_bits(float x) {
+    const uint32_t b = __float_as_uint(x);
+    return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ bool split_in_range(float x) {
+    const float a = fabsf(x);
+    return a == 0.0f || (a >= 0x1p-50f && a <= 0x1p50f);
+}
+
+// One thread per 8 elements of `count` rows of dim (multiple of 8) floats;
+// bad[row] (per_row) or bad[0] gets 1 for a value outside the range.
+__global__ void split_bf16_kernel(const float* __restrict__ src, int64_t count, int dim,
+                                  uint32_t* __restrict__ dst, uint32_t* __restrict__ bad,
+                                  int per_row) {
+    const int cpr = dim >> 3;
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= count * cpr) return;
+    const int64_t row = t / cpr;
+    const int c = (int)(t - row * cpr);
+    const float* s = src + row * dim + 8 * c;
+    const f4v a = *reinterpret_cast<const f4v*>(s);
+    const f4v b = *reinterpret_cast<const f4v*>(s + 4);
+    const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    uint32_t hi[4], lo[4];
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+        const uint32_t h0 = bf16_rne_bits(x[i]), h1 = bf16_rne_bits(x[i + 1]);
+        const float r0 = x[i] - __uint_as_float(h0 << 16);
+        const float r1 = x[i + 1] - __uint_as_float(h1 << 16);
+        hi[i / 2] = h0 | (h1 << 16);
+        lo[i / 2] = bf16_rne_bits(r0) | (bf16_rne_bits(r1) << 16);
+        ok = ok && split_in_range(x[i]) && split_in_range(x[i + 1]);
+    }
+    uint32_t* d = dst + row * dim + 8 * c;
+    *reinterpret_cast<i4v*>(d) = i4v{(int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+    *reinterpret_cast<i4v*>(d + 4) = i4v{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3]};
+    if (!ok) atomicOr(bad + (per_row ? row : 0), 1u);
+}
+
+hipError_t launch_split_bf16(const float* src, int64_t count, int dim, uint32_t* dst,
+                             uint32_t* bad, bool per_row, hipStream_t s) {
+    const int64_t threads = count * (dim / 8);
+    if (threads <= 0) return hipSuccess;
+    hipLaunchKernelGGL(split_bf16_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
+                       src, count, dim, dst, bad, per_row ? 1 : 0);
+    return hipGetLastError();
+}
+
+typedef __bf16 bf8v __attribute__((ext_vector_type(8)));
+
+template <int DIM>
+struct Bf3Shape {
+    static constexpr int NS = DIM / 16;  // MFMA k-steps per row
+    static constexpr int SL = NS <= 12 ? NS : (NS % 12 == 0 ? 12 : 8);
+    static constexpr int NSLICE = NS / SL;
+    static constexpr int RB = 64 * SL;  // bytes of a row per slice
+    static constexpr int RS = RB + 16;  // LDS row pitch: an odd number of 16-byte units
+    static constexpr int SLICE_BYTES = kGemmRows * RS;
+    static constexpr int LOADS = kGemmRows * RB / 16 / 256;  // 16-byte chunks per thread
+    static_assert(DIM % 16 == 0 && NS % SL == 0 && SL % 2 == 0, "unsupported dimension");
+};
+
+template <int DIM>
+size_t bf3_lds_bytes() {
+    return 2 * (size_t)Bf3Shape<DIM>::SLICE_BYTES + sizeof(float) * 4 * kGemmRows;
+}
+
+struct Bf3Args {
+    int nseg;
+    int nqb;
+    int64_t rows_per_seg;     // multiple of kGemmRows
+    int64_t seg_rows;         // rows scanned from each segment's start
+    float abs_slack;
+    const uint64_t* qbound;   // per query (BOUNDED)
+    uint64_t* lists;          // [nq][nseg][2][C]
+};
+
+// grid, block and lists as flat_gemm_f32.  split_rows / split_q: the split
+// parts of the rows and of the queries.
+template <int DIM, int METRIC, int C, bool BOUNDED>
+__global__ __launch_bounds__(256) void flat_gemm_bf16x3(
+    const uint32_t* __restrict__ split_rows, const float* __restrict__ norms, int64_t n,
+    const uint32_t* __restrict__ split_q, const float* __restrict__ queries, int64_t nq,
+    BoundCoef bc, Bf3Args ga) {
+    using G = Bf3Shape<DIM>;
+    constexpr int NS = G::NS, SL = G::SL, NSLICE = G::NSLICE;
+    extern __shared__ uint64_t lds[];
+    uint8_t* xs = reinterpret_cast<uint8_t*>(lds);                   // [2][32][RS]
+    float* tva = reinterpret_cast<float*>(xs + 2 * G::SLICE_BYTES);  // [2][32] vn
+    float* tvb = tva + 2 * kGemmRows;  // [2][32] sqrt(vn), or 1 / sqrt(vn) for cosine
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = lane >> 5, col = lane & 31;
+
+    const int b = blockIdx.x, grp = 8 * ga.nqb;
+    const int seg = 8 * (b / grp) + (b % 8);
+    const int qb = (b % grp) / 8;
+
+    const int64_t qid = (int64_t)qb * kGemmQueries + wave * 32 + col;
+    const bool qvalid = qid < nq;
+    const int64_t qrow = qvalid ? qid : 0;
+    bf8v qh[NS], ql[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        const uint32_t* p = split_q + qrow * DIM + 8 * (2 * s + h);
+        qh[s] = __builtin_bit_cast(bf8v, *reinterpret_cast<const i4v*>(p));
+        ql[s] = __builtin_bit_cast(bf8v, *reinterpret_cast<const i4v*>(p + 4));
+    }
+    // The query norm in the fp32 path's order (fmaf over float4 chunks).
+    float qsq = 0.0f;
+    {
+        const float* qp = queries + qrow * DIM + 4 * h;
+#pragma unroll
+        for (int g = 0; g < DIM / 8; ++g) {
+            const f4v v = *reinterpret_cast<const f4v*>(qp + 8 * g);
+            qsq = fmaf(v.x, v.x, qsq);
+            qsq = fmaf(v.y, v.y, qsq);
+            qsq = fmaf(v.z, v.z, qsq);
+            qsq = fmaf(v.w, v.w, qsq);
+        }
+    }
+    const float qn = qsq + __shfl_xor(qsq, 32);
+    const float sq = sqrtf(qn);
+    const float rq = 1.0f / sq;
+    uint64_t lst[C];
+#pragma unroll
+    for (int i = 0; i < C; ++i) lst[i] = kEmptySlot;
+    const uint64_t bound = !qvalid ? 0ull : (BOUNDED ? ga.qbound[qid] : kEmptySlot);
+    float thr = !qvalid ? -__int_as_float(0x7F800000)
+                        : (bound == kEmptySlot ? __int_as_float(0x7F800000) : slot_key(bound));
+
+    const int64_t seg0 = (int64_t)seg * ga.rows_per_seg;
+    const int64_t seg1 = seg0 + ga.seg_rows < n ? seg0 + ga.seg_rows : n;
+    const int64_t ntiles = seg1 > seg0 ? (seg1 - seg0 + kGemmRows - 1) / kGemmRows : 0;
+
+    i4v pre[G::LOADS];
+    auto load_slice = [&](int64_t tile, int part) {
+#pragma unroll
+        for (int u = 0; u < G::LOADS; ++u) {
+            const int e = tid + 256 * u;
+            const int r = e / (G::RB / 16), i = e % (G::RB / 16);
+            int64_t row = seg0 + tile * kGemmRows + r;
+            row = row < seg1 ? row : seg1 - 1;
+            pre[u] = *reinterpret_cast<const i4v*>(
+                reinterpret_cast<const uint8_t*>(split_rows + row * DIM) + part * G::RB + 16 * i);
+        }
+    };
+    auto store_slice = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < G::LOADS; ++u) {
+            const int e = tid + 256 * u;
+            const int r = e / (G::RB / 16), i = e % (G::RB / 16);
+            *reinterpret_cast<i4v*>(xs + buf * G::SLICE_BYTES + r * G::RS + 16 * i) = pre[u];
+        }
+    };
+    // Rows past the segment's end get NaN norms: their keys never pass.
+    auto load_norms = [&](int64_t tile) {
+        if (tid < kGemmRows) {
+            const int64_t row = seg0 + tile * kGemmRows + tid;
+            const bool in = row < seg1;
+            const float vn = norms[in ? row : seg1 - 1];
+            const int at = (int)(tile & 1) * kGemmRows + tid;
+            const float nan = __int_as_float(0x7FC00000);
+            tva[at] = in ? vn : nan;
+            tvb[at] = !in ? nan
+                          : (METRIC == kMetricCosine ? (vn > 0.0f ? 1.0f / sqrtf(vn) : 0.0f)
+                                                     : sqrtf(vn));
+        }
+    };
+    // Offers tile `tile`'s 16 keys per lane (tile < 0: nothing): keys
+    // branch-free, then the insertion path only for a lane with a key at
+    // or below its threshold.
+    auto offer = [&](const f16v& f, int64_t tile) {
+        if (tile < 0) return;
+        const int tb = (int)(tile & 1) * kGemmRows;
+        float key[16];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int m0 = 8 * g + 4 * h;
+            const f4v vna = *reinterpret_cast<const f4v*>(tva + tb + m0);
+            const f4v wva = *reinterpret_cast<const f4v*>(tvb + tb + m0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float fv = f[4 * g + j], vn = vna[j], wv = wva[j];
+                float k;
+                if (METRIC == kMetricIP) {
+                    k = -fv - (sq * wv) * bc.c_ip;
+                } else if (METRIC == kMetricL2) {
+                    float dd = qn - 2.0f * fv + vn;
+                    dd = dd > 0.0f ? dd : 0.0f;
+                    k = dd - (qn + vn + 2.0f * (sq * wv)) * bc.c_l2;
+                } else {
+                    k = (1.0f - fv * (rq * wv)) - bc.eps_cos;
+                    k = qn * vn < 1.03e-20f ? -1.0f : k;       // near the 1e-10 branch
+                    k = vn == 0.0f ? 1.0f - bc.eps_cos : k;    // both paths give exactly 1
+                    k = vn != vn ? vn : k;                     // past the segment: NaN
+                }
+                key[4 * g + j] = k - ga.abs_slack;
+            }
+        }
+        float mn = key[0];
+#pragma unroll
+        for (int i = 1; i < 16; ++i) mn = fminf(mn, key[i]);
+        if (mn <= thr) {
+            const int64_t base = seg0 + tile * kGemmRows;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                if (key[i] <= thr) {
+                    const int m = 8 * (i >> 2) + 4 * h + (i & 3);
+                    const uint64_t slot = pack_slot(key[i], (uint32_t)(base + m));
+                    if (slot <= bound) {
+                        list_insert<C>(lst, slot);
+                        const uint64_t top = lst[C - 1] < bound ? lst[C - 1] : bound;
+                        thr = top == kEmptySlot ? thr : slot_key(top);
+                    }
+                }
+            }
+        }
+    };
+
+    if (ntiles > 0) {
+        load_slice(0, 0);
+        store_slice(0);
+    }
+    __syncthreads();
+    int buf = 0;
+    f16v prev = {};
+    for (int64_t t = 0; t < ntiles; ++t) {
+        load_norms(t);
+        f16v hh = {}, hl = {}, lh = {};
+#pragma unroll
+        for (int part = 0; part < NSLICE; ++part) {
+            int64_t ntile = part + 1 < NSLICE ? t : t + 1;
+            int npart = part + 1 < NSLICE ? part + 1 : 0;
+            if (ntile >= ntiles) {
+                ntile = ntiles - 1;
+                npart = NSLICE - 1;
+            }
+            load_slice(ntile, npart);
+            const uint8_t* xl = xs + buf * G::SLICE_BYTES + col * G::RS + 32 * h;
+#pragma unroll
+            for (int s = 0; s < SL; ++s) {
+                const bf8v ah = __builtin_bit_cast(bf8v, *reinterpret_cast<const i4v*>(xl + 64 * s));
+                const bf8v al = __builtin_bit_cast(bf8v, *reinterpret_cast<const i4v*>(xl + 64 * s + 16));
+                const int ks = part * SL + s;
+                hh = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, qh[ks], hh, 0, 0, 0);
+                hl = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, ql[ks], hl, 0, 0, 0);
+                lh = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, qh[ks], lh, 0, 0, 0);
+            }
+            if (part == 0) offer(prev, t - 1);
+            store_slice(buf ^ 1);
+            __syncthreads();
+            buf ^= 1;
+        }
+        prev = hh + (hl + lh);
+    }
+    offer(prev, ntiles - 1);
+    if (qvalid) {
+        uint64_t* out = ga.lists + (((size_t)qid * ga.nseg + seg) * 2 + h) * C;
+#pragma unroll
+        for (int i = 0; i < C; ++i) out[i] = lst[i];
+    }
+}
+
+// grid (1, nq): bound[q] = the kc-th smallest slot of the query's sampled
+// lists (kEmptySlot when they hold fewer than kc).
+__global__ __launch_bounds__(256) void lists_kth_slot(int kc, int cap, int64_t per_query,
+                                                      const uint64_t* __restrict__ lists,
+                                                      uint64_t* __restrict__ bound) {
+    extern __shared__ uint64_t lds[];
+    const uint32_t q = blockIdx.y;
+    WaveTopK sel;
+    block_select_lists(lists + (size_t)q * per_query, per_query, lds, cap, kc, sel);
+    if (threadIdx.x == 0) bound[q] = lds[kc - 1];
+}
+
 // grid (1, nq): one block per query selects the kc smallest keys over its
 // 2 nseg lists, then the exact rescore and proof of the streaming scan.
 template <int NCH>
 __global__ __launch_bounds__(256) void flat_lists_merge(
     const float* __restrict__ rows, const float* __restrict__ norms, int64_t n, int dim,
     const float* __restrict__ queries, int metric, int kc, int cap, int nlists, int list_len,
-    const uint64_t* __restrict__ lists, FlatArgs fa) {
+    const uint64_t* __restrict__ lists, const uint64_t* __restrict__ qbound,
+    const uint32_t* __restrict__ qbad, FlatArgs fa) {
     extern __shared__ uint64_t lds[];
     __shared__ uint32_t cut_bits;
     const int lr = threadIdx.x & 15;
@@ -281,8 +590,13 @@ __global__ __launch_bounds__(256) void flat_lists_merge(
     atomicMin(&cut_bits, mine);
     WaveTopK sel;
     block_select_lists(lq, (int64_t)nlists * list_len, lds, cap, kc, sel);  // ends in a barrier
-    const float list_cut = cut_bits == 0xFFFFFFFFu ? kFltMax : from_ordered_bits(cut_bits);
+    float list_cut = cut_bits == 0xFFFFFFFFu ? kFltMax : from_ordered_bits(cut_bits);
+    // Rows above the query's bound were never admitted: their keys are >= it.
+    if (qbound && qbound[q] != kEmptySlot) list_cut = fminf(list_cut, slot_key(qbound[q]));
     final_rescore_f4<NCH>(qv, rows, norms, n, dim, metric, q, lds, kc, fa, list_cut);
+    // A query with values outside the split range has no valid keys here:
+    // the streaming scan runs it again.
+    if (threadIdx.x == 0 && qbad && qbad[q]) fa.status[q] = 1;
 }
 
 // ---------------------------------------------------------------------------
@@ -319,12 +633,101 @@ bool plan_gemm(int64_t n, int dim, int64_t nq, int kc, GemmPlan* out) {
     int64_t rps = (n + nseg - 1) / nseg;
     p.rows_per_seg = (rps + kGemmRows - 1) / kGemmRows * kGemmRows;
     p.nseg = (int)nseg;
+    // Bounding launch of the split-bf16 contraction: up to 64 segments
+    // spread over the rows, about a sixteenth of the rows in all.
+    p.s_nseg = (int)std::min<int64_t>(nseg, 64);
+    const int64_t srps = (n + p.s_nseg - 1) / p.s_nseg;
+    p.s_rows_per_seg = (srps + kGemmRows - 1) / kGemmRows * kGemmRows;
+    int64_t srows = (n / 16 / p.s_nseg + kGemmRows - 1) / kGemmRows * kGemmRows;
+    srows = std::max<int64_t>(srows, kGemmRows);
+    p.s_seg_rows = std::min(srows, p.s_rows_per_seg);
     *out = p;
     return true;
 }
 
 size_t gemm_lists_bytes(const GemmPlan& p, int64_t nq) {
     return (size_t)nq * (size_t)p.nseg * 2 * gemm_list_len(p.kc) * sizeof(uint64_t);
+}
+
+// Unit roundoff for make_bounds that covers the split-bf16 dot error
+// g = 1.024 gamma_d(2^-23) + 3.01 2^-16 + 2^-22 (gamma_d(u_eff) = g).
+static double bf3_unit_roundoff(int dim) {
+    const double u23 = 1.0 / 8388608.0;
+    const double gd = dim * u23 / (1.0 - dim * u23);
+    const double g = 1.024 * gd + 3.01 / 65536.0 + 1.0 / 4194304.0;
+    return g / ((double)dim * (1.0 + g));
+}
+
+template <int DIM, int C, bool BOUNDED>
+static void launch_bf3_dim_c(const GemmPlan& p, const uint32_t* split_rows, const float* norms,
+                             int64_t n, const uint32_t* split_q, const float* queries, int64_t nq,
+                             int metric, const Bf3Args& ga, hipStream_t s) {
+    const BoundCoef bc = make_bounds(DIM, bf3_unit_roundoff(DIM));
+    const dim3 grid((unsigned)(ga.nseg * p.nqb));
+    const size_t shmem = bf3_lds_bytes<DIM>();
+    switch (metric) {
+    case kMetricCosine:
+        hipLaunchKernelGGL((flat_gemm_bf16x3<DIM, kMetricCosine, C, BOUNDED>), grid, dim3(256), shmem,
+                           s, split_rows, norms, n, split_q, queries, nq, bc, ga);
+        break;
+    case kMetricL2:
+        hipLaunchKernelGGL((flat_gemm_bf16x3<DIM, kMetricL2, C, BOUNDED>), grid, dim3(256), shmem, s,
+                           split_rows, norms, n, split_q, queries, nq, bc, ga);
+        break;
+    default:
+        hipLaunchKernelGGL((flat_gemm_bf16x3<DIM, kMetricIP, C, BOUNDED>), grid, dim3(256), shmem, s,
+                           split_rows, norms, n, split_q, queries, nq, bc, ga);
+        break;
+    }
+}
+
+template <int DIM>
+static void launch_bf3_dim(const GemmPlan& p, bool bounded, const uint32_t* split_rows,
+                           const float* norms, int64_t n, const uint32_t* split_q,
+                           const float* queries, int64_t nq, int metric, const Bf3Args& ga,
+                           hipStream_t s) {
+    if (gemm_list_len(p.kc) == 4) {
+        if (bounded) launch_bf3_dim_c<DIM, 4, true>(p, split_rows, norms, n, split_q, queries, nq, metric, ga, s);
+        else launch_bf3_dim_c<DIM, 4, false>(p, split_rows, norms, n, split_q, queries, nq, metric, ga, s);
+    } else {
+        if (bounded) launch_bf3_dim_c<DIM, 8, true>(p, split_rows, norms, n, split_q, queries, nq, metric, ga, s);
+        else launch_bf3_dim_c<DIM, 8, false>(p, split_rows, norms, n, split_q, queries, nq, metric, ga, s);
+    }
+}
+
+hipError_t launch_flat_bf3(const GemmPlan& p, bool sampled, const uint32_t* split_rows,
+                           const float* norms, int64_t n, int dim, const uint32_t* split_q,
+                           const float* queries, int64_t nq, int metric, const uint64_t* qbound,
+                           uint64_t* lists, hipStream_t s) {
+    Bf3Args ga;
+    ga.nseg = sampled ? p.s_nseg : p.nseg;
+    ga.nqb = p.nqb;
+    ga.rows_per_seg = sampled ? p.s_rows_per_seg : p.rows_per_seg;
+    ga.seg_rows = sampled ? p.s_seg_rows : p.rows_per_seg;
+    // Products and partial sums of three chains flushed below 2^-126,
+    // counted twice for L2's -2 dot.
+    ga.abs_slack = (float)(12.0 * dim * 1.1754943508222875e-38);
+    ga.qbound = qbound;
+    ga.lists = lists;
+    const bool bounded = !sampled;
+    switch (dim) {
+    case 64: launch_bf3_dim<64>(p, bounded, split_rows, norms, n, split_q, queries, nq, metric, ga, s); break;
+    case 96: launch_bf3_dim<96>(p, bounded, split_rows, norms, n, split_q, queries, nq, metric, ga, s); break;
+    case 128: launch_bf3_dim<128>(p, bounded, split_rows, norms, n, split_q, queries, nq, metric, ga, s); break;
+    case 192: launch_bf3_dim<192>(p, bounded, split_rows, norms, n, split_q, queries, nq, metric, ga, s); break;
+    case 256: launch_bf3_dim<256>(p, bounded, split_rows, norms, n, split_q, queries, nq, metric, ga, s); break;
+    case 384: launch_bf3_dim<384>(p, bounded, split_rows, norms, n, split_q, queries, nq, metric, ga, s); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_bf3_bounds(const GemmPlan& p, int64_t nq, const uint64_t* lists, uint64_t* bound,
+                             hipStream_t s) {
+    const int64_t per_query = (int64_t)p.s_nseg * 2 * gemm_list_len(p.kc);
+    hipLaunchKernelGGL(lists_kth_slot, dim3(1, (unsigned)nq), dim3(256),
+                       sizeof(uint64_t) * 4 * (size_t)p.cap, s, p.kc, p.cap, per_query, lists, bound);
+    return hipGetLastError();
 }
 
 template <int DIM, int C>
@@ -364,11 +767,12 @@ static hipError_t launch_gemm_dim(const GemmPlan& p, const float* rows, const fl
 template <int NCH>
 static void launch_lists_merge(const GemmPlan& p, const float* rows, const float* norms, int64_t n,
                                int dim, const float* queries, int64_t nq, int metric,
-                               const uint64_t* lists, const FlatArgs& fa, hipStream_t s) {
+                               const uint64_t* lists, const uint64_t* qbound,
+                               const uint32_t* qbad, const FlatArgs& fa, hipStream_t s) {
     size_t shmem = sizeof(uint64_t) * 4 * (size_t)p.cap;
     hipLaunchKernelGGL(flat_lists_merge<NCH>, dim3(1, (unsigned)nq), dim3(256), shmem, s, rows,
                        norms, n, dim, queries, metric, p.kc, p.cap, 2 * p.nseg,
-                       gemm_list_len(p.kc), lists, fa);
+                       gemm_list_len(p.kc), lists, qbound, qbad, fa);
 }
 
 hipError_t launch_flat_gemm(const GemmPlan& p, const float* rows, const float* norms, int64_t n,
@@ -397,7 +801,8 @@ hipError_t launch_flat_gemm(const GemmPlan& p, const float* rows, const float* n
 
 hipError_t launch_flat_gemm_merge(const GemmPlan& p, const float* rows, const float* norms,
                                   int64_t n, int dim, const float* queries, int64_t nq, int metric,
-                                  const uint64_t* lists, const FlatBuffers& b, int k, int k_stride,
+                                  const uint64_t* lists, const uint64_t* qbound,
+                                  const uint32_t* qbad, const FlatBuffers& b, int k, int k_stride,
                                   hipStream_t s) {
     FlatArgs fa = {};
     fa.out_dist = b.out_dist;
@@ -406,11 +811,11 @@ hipError_t launch_flat_gemm_merge(const GemmPlan& p, const float* rows, const fl
     fa.k = k;
     fa.k_stride = k_stride;
     switch (flat_nch_for_dim(dim)) {
-    case 1: launch_lists_merge<1>(p, rows, norms, n, dim, queries, nq, metric, lists, fa, s); break;
-    case 2: launch_lists_merge<2>(p, rows, norms, n, dim, queries, nq, metric, lists, fa, s); break;
-    case 3: launch_lists_merge<3>(p, rows, norms, n, dim, queries, nq, metric, lists, fa, s); break;
-    case 4: launch_lists_merge<4>(p, rows, norms, n, dim, queries, nq, metric, lists, fa, s); break;
-    case 6: launch_lists_merge<6>(p, rows, norms, n, dim, queries, nq, metric, lists, fa, s); break;
+    case 1: launch_lists_merge<1>(p, rows, norms, n, dim, queries, nq, metric, lists, qbound, qbad, fa, s); break;
+    case 2: launch_lists_merge<2>(p, rows, norms, n, dim, queries, nq, metric, lists, qbound, qbad, fa, s); break;
+    case 3: launch_lists_merge<3>(p, rows, norms, n, dim, queries, nq, metric, lists, qbound, qbad, fa, s); break;
+    case 4: launch_lists_merge<4>(p, rows, norms, n, dim, queries, nq, metric, lists, qbound, qbad, fa, s); break;
+    case 6: launch_lists_merge<6>(p, rows, norms, n, dim, queries, nq, metric, lists, qbound, qbad, fa, s); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

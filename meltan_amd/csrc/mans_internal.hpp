@@ -45,6 +45,10 @@ struct GemmPlan {
     int nseg = 0;  // row segments, a multiple of 8
     int nqb = 0;   // blocks of 128 queries
     int64_t rows_per_seg = 0;
+    // The split-bf16 path's bounding launch over sampled rows.
+    int s_nseg = 0;
+    int64_t s_rows_per_seg = 0;
+    int64_t s_seg_rows = 0;
 };
 // False when the batch, dimension or kc does not suit the batched path.
 bool plan_gemm(int64_t n, int dim, int64_t nq, int kc, GemmPlan* out);
@@ -55,11 +59,30 @@ hipError_t launch_flat_gemm(const GemmPlan& p, const float* rows, const float* n
                             int dim, const float* queries, int64_t nq, int metric,
                             uint64_t* lists, hipStream_t s);
 // The per-query merge, exact rescore and proof: writes the k results and the
-// proof status of every query (as launch_flat_search).
+// proof status of every query (as launch_flat_search).  qbound (nullable):
+// per-query bounds of the split-bf16 path; qbad (nullable): queries whose
+// keys are not valid (status 1).
 hipError_t launch_flat_gemm_merge(const GemmPlan& p, const float* rows, const float* norms,
                                   int64_t n, int dim, const float* queries, int64_t nq, int metric,
-                                  const uint64_t* lists, const FlatBuffers& b, int k, int k_stride,
+                                  const uint64_t* lists, const uint64_t* qbound,
+                                  const uint32_t* qbad, const FlatBuffers& b, int k, int k_stride,
                                   hipStream_t s);
+
+// Split-bf16 contraction (fp32-level accuracy on bf16 MFMA).
+// Splits `count` rows of dim floats into [8 hi | 8 lo] bf16 parts per 8
+// elements; bad[row] (per_row) or bad[0] is or-ed with 1 for a value
+// outside [2^-50, 2^50] (other than 0).
+hipError_t launch_split_bf16(const float* src, int64_t count, int dim, uint32_t* dst,
+                             uint32_t* bad, bool per_row, hipStream_t s);
+// sampled: the bounding launch (no bounds); otherwise the full launch with
+// the per-query bounds qbound.  Writes the lane lists.
+hipError_t launch_flat_bf3(const GemmPlan& p, bool sampled, const uint32_t* split_rows,
+                           const float* norms, int64_t n, int dim, const uint32_t* split_q,
+                           const float* queries, int64_t nq, int metric, const uint64_t* qbound,
+                           uint64_t* lists, hipStream_t s);
+// bound[q] = the kc-th smallest slot of the sampled lists of query q.
+hipError_t launch_bf3_bounds(const GemmPlan& p, int64_t nq, const uint64_t* lists, uint64_t* bound,
+                             hipStream_t s);
 
 // target_blocks: blocks over all queries of a launch (0: the flat scan's default).
 FlatPlan plan_flat(int64_t n, int64_t nq, int kc, int64_t target_blocks = 0);

@@ -42,6 +42,7 @@ struct Slot {
     DevBuf heads;                 // block heads of the flat scan's threshold merge
     bool counters_dirty = false;  // a launch failed: re-zero the merge counters
     DevBuf aux0, aux1, aux2, aux3;
+    DevBuf qsplit, qbad;          // split-bf16 queries and their range flags
     PinnedBuf status_h, stage_h, result_h;  // pinned status, query staging, results
     ~Slot();
 };
@@ -89,6 +90,11 @@ struct mans_corpus {
     // int8 planes (Int8CodeCache.swift:22-108), built on first use.
     bool int8_valid = false;
     mans::DevBuf i8_codes, i8_u, i8_w, i8_normsq, i8_invsqrt;
+    // Split-bf16 parts of the rows for the batched contraction, built on
+    // first use; bf_ok: every value is in the split range.
+    bool bf_valid = false;
+    bool bf_ok = false;
+    mans::DevBuf bf_split, bf_flag;
 };
 
 namespace mans {
