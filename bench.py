@@ -34,6 +34,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 FP32_MFMA_TFLOPS = 157.3
+BF16_MFMA_TFLOPS = 2500.0  # dense
 METRIC = "queries/sec exact top-10 @1M×384 fp32 (batch 1/1024); p50 single-query µs @100k"
 CPU_THREADS = min(16, os.cpu_count() or 1)  # the host share of one GPU
 
@@ -73,10 +74,11 @@ def roofline_hbm(kernel, workload, bytes_per_launch, avg_s):
             "bytes_per_launch": int(bytes_per_launch)}
 
 
-def roofline_mfma(kernel, workload, flops_per_launch, avg_s):
+def roofline_mfma(kernel, workload, flops_per_launch, avg_s, peak=None):
+    peak = peak or FP32_MFMA_TFLOPS
     tf = flops_per_launch / avg_s / 1e12
-    return {"bound": "mfma", "achieved": round(tf, 2), "peak": FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(tf / FP32_MFMA_TFLOPS, 4), "traffic": measured_traffic(kernel, workload),
+    return {"bound": "mfma", "achieved": round(tf, 2), "peak": peak, "unit": "TFLOP/s",
+            "frac": round(tf / peak, 4), "traffic": measured_traffic(kernel, workload),
             "kernel": kernel, "avg_launch_us": round(avg_s * 1e6, 2),
             "flops_per_launch": int(flops_per_launch)}
 
@@ -159,8 +161,20 @@ def bench_flat(args, ctx):
         step = make_step(b)
         elapsed = timed(step, steps, warmup, hip)
         reps = min(steps, 20)
-        kt = kernel_avg(ctx, step, reps, ["flat_gemm", "flat_merge", "flat_scan"], hip)
-        if kt["flat_gemm"][1]:
+        kt = kernel_avg(ctx, step, reps, ["flat_bound", "flat_gemm", "flat_merge", "flat_scan"], hip)
+        if kt["flat_gemm"][1] and kt["flat_bound"][1]:
+            # Split-bf16 contraction: three bf16 MFMA products per fp32
+            # product.  achieved = algorithmic flops (2 B n d) / launch time
+            # against the dense bf16 peak; the issued rate is three times it.
+            avg, launches = kt["flat_gemm"]
+            flops = 2.0 * (b * reps / launches) * n * dim
+            roof = roofline_mfma("flat_gemm_bf16x3<384,cosine,4,bounded>", f"flat_{n}x{dim}_b{b}",
+                                 flops, avg, peak=BF16_MFMA_TFLOPS)
+            roof["issued_tflops"] = round(3 * flops / avg / 1e12, 2)
+            roof["issued_frac"] = round(3 * flops / avg / 1e12 / BF16_MFMA_TFLOPS, 4)
+            roof["bound_pass_us"] = round(kt["flat_bound"][0] * 1e6, 2)
+            roof["merge_avg_us"] = round(kt["flat_merge"][0] * 1e6, 2) if kt["flat_merge"][1] else None
+        elif kt["flat_gemm"][1]:
             avg, launches = kt["flat_gemm"]
             flops = 2.0 * (b * reps / launches) * n * dim  # queries per launch x n x d
             roof = roofline_mfma("flat_gemm_f32<384,cosine>", f"flat_{n}x{dim}_b{b}", flops, avg)

@@ -333,21 +333,32 @@ hipError_t launch_split_bf16(const float* src, int64_t count, int dim, uint32_t*
 
 typedef __bf16 bf8v __attribute__((ext_vector_type(8)));
 
+// Row slices reach LDS by direct global-to-LDS loads (global_load_lds,
+// 16 bytes per lane), NBUF slices in flight: the loads run ahead of the
+// MFMAs without holding registers.  A slice is 32 rows x CPR 16-byte
+// chunks, unpadded; chunk c of row r sits at c ^ (r & SWZ), so the 32 lanes
+// of a half-wave reading one chunk of 32 rows hit distinct banks.
+constexpr int kBf3Buf = 4;
+
 template <int DIM>
 struct Bf3Shape {
     static constexpr int NS = DIM / 16;  // MFMA k-steps per row
     static constexpr int SL = NS <= 12 ? NS : (NS % 12 == 0 ? 12 : 8);
     static constexpr int NSLICE = NS / SL;
-    static constexpr int RB = 64 * SL;  // bytes of a row per slice
-    static constexpr int RS = RB + 16;  // LDS row pitch: an odd number of 16-byte units
-    static constexpr int SLICE_BYTES = kGemmRows * RS;
-    static constexpr int LOADS = kGemmRows * RB / 16 / 256;  // 16-byte chunks per thread
+    static constexpr int RB = 64 * SL;   // bytes of a row per slice
+    static constexpr int CPR = 4 * SL;   // 16-byte chunks of a row per slice
+    static constexpr int LOWBIT = CPR & -CPR;
+    static constexpr int SWZ = (LOWBIT < 16 ? LOWBIT : 16) - 1;
+    static constexpr int SLICE_BYTES = kGemmRows * RB;
+    static constexpr int WAVE_INSTS = kGemmRows * CPR / 64 / 4;  // loads per wave per slice
     static_assert(DIM % 16 == 0 && NS % SL == 0 && SL % 2 == 0, "unsupported dimension");
+    static_assert(WAVE_INSTS * 256 == kGemmRows * CPR, "slice does not split over 4 waves");
 };
 
 template <int DIM>
 size_t bf3_lds_bytes() {
-    return 2 * (size_t)Bf3Shape<DIM>::SLICE_BYTES + sizeof(float) * 4 * kGemmRows;
+    return kBf3Buf * (size_t)Bf3Shape<DIM>::SLICE_BYTES +
+           sizeof(float) * (kBf3Buf * kGemmRows + 4 * kGemmRows);
 }
 
 struct Bf3Args {
@@ -360,6 +371,14 @@ struct Bf3Args {
     uint64_t* lists;          // [nq][nseg][2][C]
 };
 
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt out of range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 // grid, block and lists as flat_gemm_f32.  split_rows / split_q: the split
 // parts of the rows and of the queries.
 template <int DIM, int METRIC, int C, bool BOUNDED>
@@ -368,11 +387,12 @@ __global__ __launch_bounds__(256) void flat_gemm_bf16x3(
     const uint32_t* __restrict__ split_q, const float* __restrict__ queries, int64_t nq,
     BoundCoef bc, Bf3Args ga) {
     using G = Bf3Shape<DIM>;
-    constexpr int NS = G::NS, SL = G::SL, NSLICE = G::NSLICE;
+    constexpr int NS = G::NS, SL = G::SL, NSLICE = G::NSLICE, CPR = G::CPR, SWZ = G::SWZ;
     extern __shared__ uint64_t lds[];
-    uint8_t* xs = reinterpret_cast<uint8_t*>(lds);                   // [2][32][RS]
-    float* tva = reinterpret_cast<float*>(xs + 2 * G::SLICE_BYTES);  // [2][32] vn
-    float* tvb = tva + 2 * kGemmRows;  // [2][32] sqrt(vn), or 1 / sqrt(vn) for cosine
+    uint8_t* ring = reinterpret_cast<uint8_t*>(lds);                    // [NBUF][32][CPR][16]
+    float* tvn = reinterpret_cast<float*>(ring + kBf3Buf * G::SLICE_BYTES);  // [NBUF][32] raw vn
+    float* tva = tvn + kBf3Buf * kGemmRows;  // [2][32] vn (NaN past the segment)
+    float* tvb = tva + 2 * kGemmRows;        // [2][32] sqrt(vn), or 1 / sqrt(vn) for cosine
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = lane >> 5, col = lane & 31;
 
@@ -387,8 +407,14 @@ __global__ __launch_bounds__(256) void flat_gemm_bf16x3(
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
         const uint32_t* p = split_q + qrow * DIM + 8 * (2 * s + h);
-        qh[s] = __builtin_bit_cast(bf8v, *reinterpret_cast<const i4v*>(p));
-        ql[s] = __builtin_bit_cast(bf8v, *reinterpret_cast<const i4v*>(p + 4));
+        i4v a = *reinterpret_cast<const i4v*>(p);
+        i4v c = *reinterpret_cast<const i4v*>(p + 4);
+        // Opaque to the compiler: kept in registers rather than reloaded
+        // from memory inside the loop (a reload would wait on the vector
+        // memory counter, which the slice loads in flight also occupy).
+        asm volatile("" : "+v"(a), "+v"(c));
+        qh[s] = __builtin_bit_cast(bf8v, a);
+        ql[s] = __builtin_bit_cast(bf8v, c);
     }
     // The query norm in the fp32 path's order (fmaf over float4 chunks).
     float qsq = 0.0f;
@@ -406,6 +432,10 @@ __global__ __launch_bounds__(256) void flat_gemm_bf16x3(
     const float qn = qsq + __shfl_xor(qsq, 32);
     const float sq = sqrtf(qn);
     const float rq = 1.0f / sq;
+    // Cosine rows with qn vn below 1.03e-20 get the key -1 (the formula's
+    // 1e-10 branch is near); vn below this threshold covers every such row.
+    const float vn_tiny = (1.03e-20f / qn) * 1.0001f;
+    const float eps_all = bc.eps_cos + ga.abs_slack;
     uint64_t lst[C];
 #pragma unroll
     for (int i = 0; i < C; ++i) lst[i] = kEmptySlot;
@@ -416,39 +446,34 @@ __global__ __launch_bounds__(256) void flat_gemm_bf16x3(
     const int64_t seg0 = (int64_t)seg * ga.rows_per_seg;
     const int64_t seg1 = seg0 + ga.seg_rows < n ? seg0 + ga.seg_rows : n;
     const int64_t ntiles = seg1 > seg0 ? (seg1 - seg0 + kGemmRows - 1) / kGemmRows : 0;
+    const int64_t total = ntiles * NSLICE;  // slices
 
-    i4v pre[G::LOADS];
-    auto load_slice = [&](int64_t tile, int part) {
+    // Loads slice j (tile j / NSLICE, part j % NSLICE) into ring buffer
+    // j % NBUF, and with a tile's first slice its row norms.  Rows past the
+    // segment's end load its last row.
+    auto issue = [&](int64_t j) {
+        if (j >= total) return;
+        const int64_t tile = j / NSLICE;
+        const int part = (int)(j - tile * NSLICE);
+        uint8_t* base = ring + (int)(j % kBf3Buf) * G::SLICE_BYTES;
 #pragma unroll
-        for (int u = 0; u < G::LOADS; ++u) {
-            const int e = tid + 256 * u;
-            const int r = e / (G::RB / 16), i = e % (G::RB / 16);
+        for (int u = 0; u < G::WAVE_INSTS; ++u) {
+            const int inst = wave * G::WAVE_INSTS + u;
+            const int p = inst * 64 + lane;
+            const int r = p / CPR, qq = p - r * CPR;
+            const int c = qq ^ (r & SWZ);
             int64_t row = seg0 + tile * kGemmRows + r;
             row = row < seg1 ? row : seg1 - 1;
-            pre[u] = *reinterpret_cast<const i4v*>(
-                reinterpret_cast<const uint8_t*>(split_rows + row * DIM) + part * G::RB + 16 * i);
+            const uint8_t* src =
+                reinterpret_cast<const uint8_t*>(split_rows + row * DIM) + part * G::RB + 16 * c;
+            __builtin_amdgcn_global_load_lds(src, (lds_ptr_t)(base + inst * 1024), 16, 0, 0);
         }
-    };
-    auto store_slice = [&](int buf) {
-#pragma unroll
-        for (int u = 0; u < G::LOADS; ++u) {
-            const int e = tid + 256 * u;
-            const int r = e / (G::RB / 16), i = e % (G::RB / 16);
-            *reinterpret_cast<i4v*>(xs + buf * G::SLICE_BYTES + r * G::RS + 16 * i) = pre[u];
-        }
-    };
-    // Rows past the segment's end get NaN norms: their keys never pass.
-    auto load_norms = [&](int64_t tile) {
-        if (tid < kGemmRows) {
-            const int64_t row = seg0 + tile * kGemmRows + tid;
-            const bool in = row < seg1;
-            const float vn = norms[in ? row : seg1 - 1];
-            const int at = (int)(tile & 1) * kGemmRows + tid;
-            const float nan = __int_as_float(0x7FC00000);
-            tva[at] = in ? vn : nan;
-            tvb[at] = !in ? nan
-                          : (METRIC == kMetricCosine ? (vn > 0.0f ? 1.0f / sqrtf(vn) : 0.0f)
-                                                     : sqrtf(vn));
+        if (part == 0 && wave == 0 && lane < kGemmRows) {
+            int64_t row = seg0 + tile * kGemmRows + lane;
+            row = row < seg1 ? row : seg1 - 1;
+            __builtin_amdgcn_global_load_lds(norms + row,
+                                             (lds_ptr_t)(tvn + (int)(tile % kBf3Buf) * kGemmRows),
+                                             4, 0, 0);
         }
     };
     // Offers tile `tile`'s 16 keys per lane (tile < 0: nothing): keys
@@ -468,18 +493,18 @@ __global__ __launch_bounds__(256) void flat_gemm_bf16x3(
                 const float fv = f[4 * g + j], vn = vna[j], wv = wva[j];
                 float k;
                 if (METRIC == kMetricIP) {
-                    k = -fv - (sq * wv) * bc.c_ip;
+                    k = (-fv - (sq * wv) * bc.c_ip) - ga.abs_slack;
                 } else if (METRIC == kMetricL2) {
                     float dd = qn - 2.0f * fv + vn;
                     dd = dd > 0.0f ? dd : 0.0f;
-                    k = dd - (qn + vn + 2.0f * (sq * wv)) * bc.c_l2;
+                    k = (dd - (qn + vn + 2.0f * (sq * wv)) * bc.c_l2) - ga.abs_slack;
                 } else {
-                    k = (1.0f - fv * (rq * wv)) - bc.eps_cos;
-                    k = qn * vn < 1.03e-20f ? -1.0f : k;       // near the 1e-10 branch
-                    k = vn == 0.0f ? 1.0f - bc.eps_cos : k;    // both paths give exactly 1
-                    k = vn != vn ? vn : k;                     // past the segment: NaN
+                    // A zero row has wv = 0 and key 1 - eps (both paths give
+                    // exactly 1); past the segment vn and wv are NaN.
+                    k = (1.0f - fv * (rq * wv)) - eps_all;
+                    k = vn < vn_tiny ? -1.0f : k;
                 }
-                key[4 * g + j] = k - ga.abs_slack;
+                key[4 * g + j] = k;
             }
         }
         float mn = key[0];
@@ -502,42 +527,72 @@ __global__ __launch_bounds__(256) void flat_gemm_bf16x3(
         }
     };
 
-    if (ntiles > 0) {
-        load_slice(0, 0);
-        store_slice(0);
-    }
-    __syncthreads();
-    int buf = 0;
+#pragma unroll
+    for (int j = 0; j < kBf3Buf - 1; ++j) issue(j);
     f16v prev = {};
     for (int64_t t = 0; t < ntiles; ++t) {
-        load_norms(t);
         f16v hh = {}, hl = {}, lh = {};
 #pragma unroll
         for (int part = 0; part < NSLICE; ++part) {
-            int64_t ntile = part + 1 < NSLICE ? t : t + 1;
-            int npart = part + 1 < NSLICE ? part + 1 : 0;
-            if (ntile >= ntiles) {
-                ntile = ntiles - 1;
-                npart = NSLICE - 1;
+            const int64_t j = t * NSLICE + part;
+            // Slice j is in LDS once at most the later slices' loads are
+            // outstanding; the barrier publishes it and frees buffer
+            // (j - 1) % NBUF, which the next load refills.
+            wait_vmcnt<(kBf3Buf - 2) * G::WAVE_INSTS>();
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            issue(j + kBf3Buf - 1);
+            if (part == 0 && wave == 0 && lane < kGemmRows) {
+                const int64_t row = seg0 + t * kGemmRows + lane;
+                const float vn = tvn[(int)(t % kBf3Buf) * kGemmRows + lane];
+                const bool in = row < seg1;
+                const float nan = __int_as_float(0x7FC00000);
+                const int at = (int)(t & 1) * kGemmRows + lane;
+                tva[at] = in ? vn : nan;
+                tvb[at] = !in ? nan
+                              : (METRIC == kMetricCosine ? (vn > 0.0f ? 1.0f / sqrtf(vn) : 0.0f)
+                                                         : sqrtf(vn));
             }
-            load_slice(ntile, npart);
-            const uint8_t* xl = xs + buf * G::SLICE_BYTES + col * G::RS + 32 * h;
+            const uint8_t* xl = ring + (int)(j % kBf3Buf) * G::SLICE_BYTES + col * CPR * 16;
+            const int sw = col & SWZ;
+            // The row operands are read two steps ahead of their MFMAs.
+            auto rd = [&](int s, int lo) {
+                return *reinterpret_cast<const i4v*>(xl + 16 * ((4 * s + 2 * h + lo) ^ sw));
+            };
+            i4v h0 = rd(0, 0), l0 = rd(0, 1);
+            i4v h1 = SL > 1 ? rd(1, 0) : h0, l1 = SL > 1 ? rd(1, 1) : l0;
 #pragma unroll
             for (int s = 0; s < SL; ++s) {
-                const bf8v ah = __builtin_bit_cast(bf8v, *reinterpret_cast<const i4v*>(xl + 64 * s));
-                const bf8v al = __builtin_bit_cast(bf8v, *reinterpret_cast<const i4v*>(xl + 64 * s + 16));
+                const bf8v ah = __builtin_bit_cast(bf8v, h0);
+                const bf8v al = __builtin_bit_cast(bf8v, l0);
+                h0 = h1;
+                l0 = l1;
+                if (s + 2 < SL) {
+                    h1 = rd(s + 2, 0);
+                    l1 = rd(s + 2, 1);
+                }
                 const int ks = part * SL + s;
                 hh = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, qh[ks], hh, 0, 0, 0);
                 hl = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, ql[ks], hl, 0, 0, 0);
                 lh = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, qh[ks], lh, 0, 0, 0);
             }
+            // Schedule: each step's two LDS reads (for the step two ahead)
+            // between its three MFMAs.
+#pragma unroll
+            for (int s = 0; s < SL; ++s) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if (s + 2 < SL) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if (s + 2 < SL) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            }
+            // The previous tile's keys (its norms were published by the
+            // barrier of this tile's first slice), while the MFMAs run.
             if (part == 0) offer(prev, t - 1);
-            store_slice(buf ^ 1);
-            __syncthreads();
-            buf ^= 1;
         }
         prev = hh + (hl + lh);
     }
+    __syncthreads();  // the last tile's norms
     offer(prev, ntiles - 1);
     if (qvalid) {
         uint64_t* out = ga.lists + (((size_t)qid * ga.nseg + seg) * 2 + h) * C;
@@ -665,6 +720,16 @@ static void launch_bf3_dim_c(const GemmPlan& p, const uint32_t* split_rows, cons
     const BoundCoef bc = make_bounds(DIM, bf3_unit_roundoff(DIM));
     const dim3 grid((unsigned)(ga.nseg * p.nqb));
     const size_t shmem = bf3_lds_bytes<DIM>();
+    static bool attr = [] {
+        (void)hipFuncSetAttribute((const void*)flat_gemm_bf16x3<DIM, kMetricCosine, C, BOUNDED>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)bf3_lds_bytes<DIM>());
+        (void)hipFuncSetAttribute((const void*)flat_gemm_bf16x3<DIM, kMetricL2, C, BOUNDED>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)bf3_lds_bytes<DIM>());
+        (void)hipFuncSetAttribute((const void*)flat_gemm_bf16x3<DIM, kMetricIP, C, BOUNDED>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)bf3_lds_bytes<DIM>());
+        return true;
+    }();
+    (void)attr;
     switch (metric) {
     case kMetricCosine:
         hipLaunchKernelGGL((flat_gemm_bf16x3<DIM, kMetricCosine, C, BOUNDED>), grid, dim3(256), shmem,
