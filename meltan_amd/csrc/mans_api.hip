@@ -443,6 +443,7 @@ static int flat_search_chunk(mans_ctx* ctx, const mans_corpus* c, const float* d
             // First round of a batch: MFMA contraction + per-query merge,
             // on split-bf16 MFMA when the corpus allows it, else fp32 MFMA.
             const bool bf3 = bf3_enabled() && bf16_split_ensure(ctx, c, st) == MANS_OK && c->bf_ok;
+            if (bf3) gp.lps = 4;
             const size_t lbytes = gemm_lists_bytes(gp, npend);
             e = slot->cand.ensure(lbytes + (size_t)npend * sizeof(uint64_t), ctx->fail_alloc);
             if (e == hipSuccess) e = slot->status.ensure((size_t)npend, ctx->fail_alloc);

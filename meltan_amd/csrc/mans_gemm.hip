@@ -3,6 +3,7 @@
 // contraction with the top-k selection fused into its epilogue, followed by
 // the per-query merge, exact rescore and proof of the streaming scan.
 #include <algorithm>
+#include <type_traits>
 #include <cstdlib>
 
 #include "mans_device.hpp"
@@ -333,32 +334,43 @@ hipError_t launch_split_bf16(const float* src, int64_t count, int dim, uint32_t*
 
 typedef __bf16 bf8v __attribute__((ext_vector_type(8)));
 
-// Row slices reach LDS by direct global-to-LDS loads (global_load_lds,
-// 16 bytes per lane), NBUF slices in flight: the loads run ahead of the
-// MFMAs without holding registers.  A slice is 32 rows x CPR 16-byte
-// chunks, unpadded; chunk c of row r sits at c ^ (r & SWZ), so the 32 lanes
-// of a half-wave reading one chunk of 32 rows hit distinct banks.
-constexpr int kBf3Buf = 4;
+// Work split.  A block of 8 waves serves 128 queries over one segment of
+// rows: wave w takes query group w & 3 (32 queries) and half w >> 2 of the
+// k range, so a wave keeps only its half of the query's split parts in
+// registers and two waves fit on a SIMD (one hides the other's latencies).
+// Per 32-row tile the two halves' sums (hh + (hl + lh) over each half) are
+// exchanged through LDS and added (the same IEEE sum in either wave), and
+// each wave keys 8 of the 16 rows a lane holds, keeping its own lane lists
+// (4 lists per query and segment: half x lane half).
+//
+// Tiles reach LDS by direct global-to-LDS loads (global_load_lds, 16 bytes
+// per lane) into a ring of two tile slots: tile t + 1 loads while tile t is
+// contracted, without holding registers.  A slot holds, per k half, 32 rows
+// x CPR 16-byte chunks unpadded; chunk c of row r sits at c ^ (r & SWZ), so
+// the 32 lanes of a half-wave reading one chunk of 32 rows hit distinct
+// banks.
+constexpr int kBf3Waves = 8;
+constexpr int kBf3Slots = 2;
+constexpr int kBf3Lists = 4;  // lane lists per query and segment
 
 template <int DIM>
 struct Bf3Shape {
     static constexpr int NS = DIM / 16;  // MFMA k-steps per row
-    static constexpr int SL = NS <= 12 ? NS : (NS % 12 == 0 ? 12 : 8);
-    static constexpr int NSLICE = NS / SL;
-    static constexpr int RB = 64 * SL;   // bytes of a row per slice
-    static constexpr int CPR = 4 * SL;   // 16-byte chunks of a row per slice
+    static constexpr int NH = NS / 2;    // k-steps per half
+    static constexpr int CPR = 4 * NH;   // 16-byte chunks of a row per half
     static constexpr int LOWBIT = CPR & -CPR;
     static constexpr int SWZ = (LOWBIT < 16 ? LOWBIT : 16) - 1;
-    static constexpr int SLICE_BYTES = kGemmRows * RB;
-    static constexpr int WAVE_INSTS = kGemmRows * CPR / 64 / 4;  // loads per wave per slice
-    static_assert(DIM % 16 == 0 && NS % SL == 0 && SL % 2 == 0, "unsupported dimension");
-    static_assert(WAVE_INSTS * 256 == kGemmRows * CPR, "slice does not split over 4 waves");
+    static constexpr int HALF_CHUNKS = kGemmRows * CPR;
+    static constexpr int TILE_CHUNKS = 2 * HALF_CHUNKS;
+    static constexpr int TILE_BYTES = 16 * TILE_CHUNKS;
+    static constexpr int WAVE_INSTS = (TILE_CHUNKS + 64 * kBf3Waves - 1) / (64 * kBf3Waves);
+    static_assert(DIM % 32 == 0, "unsupported dimension");
 };
 
 template <int DIM>
 size_t bf3_lds_bytes() {
-    return kBf3Buf * (size_t)Bf3Shape<DIM>::SLICE_BYTES +
-           sizeof(float) * (kBf3Buf * kGemmRows + 4 * kGemmRows);
+    return kBf3Slots * (size_t)Bf3Shape<DIM>::TILE_BYTES +
+           sizeof(float) * (kBf3Waves * 64 * 8 + kBf3Slots * kGemmRows + 4 * kGemmRows);
 }
 
 struct Bf3Args {
@@ -368,7 +380,7 @@ struct Bf3Args {
     int64_t seg_rows;         // rows scanned from each segment's start
     float abs_slack;
     const uint64_t* qbound;   // per query (BOUNDED)
-    uint64_t* lists;          // [nq][nseg][2][C]
+    uint64_t* lists;          // [nq][nseg][kBf3Lists][C]
 };
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
@@ -379,42 +391,38 @@ __device__ __forceinline__ void wait_vmcnt() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// grid, block and lists as flat_gemm_f32.  split_rows / split_q: the split
-// parts of the rows and of the queries.
+// grid: nseg * nqb blocks (1-D, XCD mapping as flat_gemm_f32); block 512.
+// split_rows / split_q: the split parts of the rows and of the queries.
 template <int DIM, int METRIC, int C, bool BOUNDED>
-__global__ __launch_bounds__(256) void flat_gemm_bf16x3(
+__global__ __launch_bounds__(512, 1) void flat_gemm_bf16x3(
     const uint32_t* __restrict__ split_rows, const float* __restrict__ norms, int64_t n,
     const uint32_t* __restrict__ split_q, const float* __restrict__ queries, int64_t nq,
     BoundCoef bc, Bf3Args ga) {
     using G = Bf3Shape<DIM>;
-    constexpr int NS = G::NS, SL = G::SL, NSLICE = G::NSLICE, CPR = G::CPR, SWZ = G::SWZ;
+    constexpr int NH = G::NH, CPR = G::CPR, SWZ = G::SWZ;
     extern __shared__ uint64_t lds[];
-    uint8_t* ring = reinterpret_cast<uint8_t*>(lds);                    // [NBUF][32][CPR][16]
-    float* tvn = reinterpret_cast<float*>(ring + kBf3Buf * G::SLICE_BYTES);  // [NBUF][32] raw vn
-    float* tva = tvn + kBf3Buf * kGemmRows;  // [2][32] vn (NaN past the segment)
-    float* tvb = tva + 2 * kGemmRows;        // [2][32] sqrt(vn), or 1 / sqrt(vn) for cosine
+    uint8_t* ring = reinterpret_cast<uint8_t*>(lds);                      // [slot][half][32][CPR][16]
+    float* xch = reinterpret_cast<float*>(ring + kBf3Slots * G::TILE_BYTES);  // [wave][64][8]
+    float* tvn = xch + kBf3Waves * 64 * 8;   // [slot][32] raw vn
+    float* tva = tvn + kBf3Slots * kGemmRows;  // [2][32] vn (NaN past the segment)
+    float* tvb = tva + 2 * kGemmRows;          // [2][32] sqrt(vn), or 1 / sqrt(vn) for cosine
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int qg = wave & 3, kp = wave >> 2;
     const int h = lane >> 5, col = lane & 31;
 
     const int b = blockIdx.x, grp = 8 * ga.nqb;
     const int seg = 8 * (b / grp) + (b % 8);
     const int qb = (b % grp) / 8;
 
-    const int64_t qid = (int64_t)qb * kGemmQueries + wave * 32 + col;
+    const int64_t qid = (int64_t)qb * kGemmQueries + qg * 32 + col;
     const bool qvalid = qid < nq;
     const int64_t qrow = qvalid ? qid : 0;
-    bf8v qh[NS], ql[NS];
+    bf8v qh[NH], ql[NH];
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-        const uint32_t* p = split_q + qrow * DIM + 8 * (2 * s + h);
-        i4v a = *reinterpret_cast<const i4v*>(p);
-        i4v c = *reinterpret_cast<const i4v*>(p + 4);
-        // Opaque to the compiler: kept in registers rather than reloaded
-        // from memory inside the loop (a reload would wait on the vector
-        // memory counter, which the slice loads in flight also occupy).
-        asm volatile("" : "+v"(a), "+v"(c));
-        qh[s] = __builtin_bit_cast(bf8v, a);
-        ql[s] = __builtin_bit_cast(bf8v, c);
+    for (int s = 0; s < NH; ++s) {
+        const uint32_t* p = split_q + qrow * DIM + 8 * (2 * (kp * NH + s) + h);
+        qh[s] = __builtin_bit_cast(bf8v, *reinterpret_cast<const i4v*>(p));
+        ql[s] = __builtin_bit_cast(bf8v, *reinterpret_cast<const i4v*>(p + 4));
     }
     // The query norm in the fp32 path's order (fmaf over float4 chunks).
     float qsq = 0.0f;
@@ -446,46 +454,66 @@ __global__ __launch_bounds__(256) void flat_gemm_bf16x3(
     const int64_t seg0 = (int64_t)seg * ga.rows_per_seg;
     const int64_t seg1 = seg0 + ga.seg_rows < n ? seg0 + ga.seg_rows : n;
     const int64_t ntiles = seg1 > seg0 ? (seg1 - seg0 + kGemmRows - 1) / kGemmRows : 0;
-    const int64_t total = ntiles * NSLICE;  // slices
 
-    // Loads slice j (tile j / NSLICE, part j % NSLICE) into ring buffer
-    // j % NBUF, and with a tile's first slice its row norms.  Rows past the
-    // segment's end load its last row.
-    auto issue = [&](int64_t j) {
-        if (j >= total) return;
-        const int64_t tile = j / NSLICE;
-        const int part = (int)(j - tile * NSLICE);
-        uint8_t* base = ring + (int)(j % kBf3Buf) * G::SLICE_BYTES;
+    // Loads tile t into slot t % 2 (both k halves), and its row norms.  Rows
+    // past the segment's end load its last row.
+    auto issue = [&](int64_t t) {
+        if (t >= ntiles) return;
+        uint8_t* base = ring + (int)(t % kBf3Slots) * G::TILE_BYTES;
 #pragma unroll
         for (int u = 0; u < G::WAVE_INSTS; ++u) {
             const int inst = wave * G::WAVE_INSTS + u;
             const int p = inst * 64 + lane;
-            const int r = p / CPR, qq = p - r * CPR;
-            const int c = qq ^ (r & SWZ);
-            int64_t row = seg0 + tile * kGemmRows + r;
-            row = row < seg1 ? row : seg1 - 1;
-            const uint8_t* src =
-                reinterpret_cast<const uint8_t*>(split_rows + row * DIM) + part * G::RB + 16 * c;
-            __builtin_amdgcn_global_load_lds(src, (lds_ptr_t)(base + inst * 1024), 16, 0, 0);
+            if (G::TILE_CHUNKS % (64 * kBf3Waves) == 0 || p < G::TILE_CHUNKS) {
+                const int half = p / G::HALF_CHUNKS, rem = p - half * G::HALF_CHUNKS;
+                const int r = rem / CPR, qq = rem - r * CPR;
+                const int c = qq ^ (r & SWZ);
+                int64_t row = seg0 + t * kGemmRows + r;
+                row = row < seg1 ? row : seg1 - 1;
+                const uint8_t* src = reinterpret_cast<const uint8_t*>(split_rows + row * DIM) +
+                                     half * (16 * CPR) + 16 * c;
+                __builtin_amdgcn_global_load_lds(src, (lds_ptr_t)(base + inst * 1024), 16, 0, 0);
+            }
         }
-        if (part == 0 && wave == 0 && lane < kGemmRows) {
-            int64_t row = seg0 + tile * kGemmRows + lane;
+        if (wave == 0 && lane < kGemmRows) {
+            int64_t row = seg0 + t * kGemmRows + lane;
             row = row < seg1 ? row : seg1 - 1;
             __builtin_amdgcn_global_load_lds(norms + row,
-                                             (lds_ptr_t)(tvn + (int)(tile % kBf3Buf) * kGemmRows),
+                                             (lds_ptr_t)(tvn + (int)(t % kBf3Slots) * kGemmRows),
                                              4, 0, 0);
         }
     };
-    // Offers tile `tile`'s 16 keys per lane (tile < 0: nothing): keys
-    // branch-free, then the insertion path only for a lane with a key at
-    // or below its threshold.
-    auto offer = [&](const f16v& f, int64_t tile) {
-        if (tile < 0) return;
-        const int tb = (int)(tile & 1) * kGemmRows;
-        float key[16];
+
+    // Sends the partner half the 8 sums it keys, receives the 8 this wave
+    // keys (rows 8 (v / 4) + 4 h + v % 4, v = 8 KP .. 8 KP + 7), adds them
+    // and offers the keys: branch-free, then the insertion path only for a
+    // lane with a key at or below its threshold.
+    auto exchange_and_offer = [&](const f16v& part, int64_t t, auto kpc) {
+        constexpr int KP = decltype(kpc)::value;
+        constexpr int other = 8 * (1 - KP), my0 = 8 * KP;
+        float* mine = xch + (wave * 64 + lane) * 8;
+        *reinterpret_cast<f4v*>(mine) = f4v{part[other], part[other + 1], part[other + 2], part[other + 3]};
+        *reinterpret_cast<f4v*>(mine + 4) =
+            f4v{part[other + 4], part[other + 5], part[other + 6], part[other + 7]};
+        // A barrier without the vector-memory wait of __syncthreads: the
+        // next tile's loads stay in flight.
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        const float* theirs = xch + (((wave + 4) & 7) * 64 + lane) * 8;
+        const f4v r0 = *reinterpret_cast<const f4v*>(theirs);
+        const f4v r1 = *reinterpret_cast<const f4v*>(theirs + 4);
+        float f[8];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int m0 = 8 * g + 4 * h;
+        for (int i = 0; i < 4; ++i) {
+            f[i] = part[my0 + i] + r0[i];
+            f[4 + i] = part[my0 + 4 + i] + r1[i];
+        }
+        const int tb = (int)(t & 1) * kGemmRows;
+        float key[8];
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            const int m0 = 8 * ((my0 >> 2) + g) + 4 * h;
             const f4v vna = *reinterpret_cast<const f4v*>(tva + tb + m0);
             const f4v wva = *reinterpret_cast<const f4v*>(tvb + tb + m0);
 #pragma unroll
@@ -509,13 +537,14 @@ __global__ __launch_bounds__(256) void flat_gemm_bf16x3(
         }
         float mn = key[0];
 #pragma unroll
-        for (int i = 1; i < 16; ++i) mn = fminf(mn, key[i]);
+        for (int i = 1; i < 8; ++i) mn = fminf(mn, key[i]);
         if (mn <= thr) {
-            const int64_t base = seg0 + tile * kGemmRows;
+            const int64_t base = seg0 + t * kGemmRows;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
+            for (int i = 0; i < 8; ++i) {
                 if (key[i] <= thr) {
-                    const int m = 8 * (i >> 2) + 4 * h + (i & 3);
+                    const int v = my0 + i;
+                    const int m = 8 * (v >> 2) + 4 * h + (v & 3);
                     const uint64_t slot = pack_slot(key[i], (uint32_t)(base + m));
                     if (slot <= bound) {
                         list_insert<C>(lst, slot);
@@ -527,75 +556,46 @@ __global__ __launch_bounds__(256) void flat_gemm_bf16x3(
         }
     };
 
-#pragma unroll
-    for (int j = 0; j < kBf3Buf - 1; ++j) issue(j);
-    f16v prev = {};
+    issue(0);
     for (int64_t t = 0; t < ntiles; ++t) {
+        // Tile t is in LDS once this wave's loads are done; the barrier
+        // publishes every wave's part and frees the other slot (tile t - 1).
+        wait_vmcnt<0>();
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        issue(t + 1);
+        if (wave == 0 && lane < kGemmRows) {
+            const int64_t row = seg0 + t * kGemmRows + lane;
+            const float vn = tvn[(int)(t % kBf3Slots) * kGemmRows + lane];
+            const bool in = row < seg1;
+            const float nan = __int_as_float(0x7FC00000);
+            const int at = (int)(t & 1) * kGemmRows + lane;
+            tva[at] = in ? vn : nan;
+            tvb[at] = !in ? nan
+                          : (METRIC == kMetricCosine ? (vn > 0.0f ? 1.0f / sqrtf(vn) : 0.0f)
+                                                     : sqrtf(vn));
+        }
+        const uint8_t* xl = ring + (int)(t % kBf3Slots) * G::TILE_BYTES +
+                            kp * (16 * G::HALF_CHUNKS) + col * CPR * 16;
+        const int sw = col & SWZ;
         f16v hh = {}, hl = {}, lh = {};
 #pragma unroll
-        for (int part = 0; part < NSLICE; ++part) {
-            const int64_t j = t * NSLICE + part;
-            // Slice j is in LDS once at most the later slices' loads are
-            // outstanding; the barrier publishes it and frees buffer
-            // (j - 1) % NBUF, which the next load refills.
-            wait_vmcnt<(kBf3Buf - 2) * G::WAVE_INSTS>();
-            __builtin_amdgcn_s_barrier();
-            asm volatile("" ::: "memory");
-            issue(j + kBf3Buf - 1);
-            if (part == 0 && wave == 0 && lane < kGemmRows) {
-                const int64_t row = seg0 + t * kGemmRows + lane;
-                const float vn = tvn[(int)(t % kBf3Buf) * kGemmRows + lane];
-                const bool in = row < seg1;
-                const float nan = __int_as_float(0x7FC00000);
-                const int at = (int)(t & 1) * kGemmRows + lane;
-                tva[at] = in ? vn : nan;
-                tvb[at] = !in ? nan
-                              : (METRIC == kMetricCosine ? (vn > 0.0f ? 1.0f / sqrtf(vn) : 0.0f)
-                                                         : sqrtf(vn));
-            }
-            const uint8_t* xl = ring + (int)(j % kBf3Buf) * G::SLICE_BYTES + col * CPR * 16;
-            const int sw = col & SWZ;
-            // The row operands are read two steps ahead of their MFMAs.
-            auto rd = [&](int s, int lo) {
-                return *reinterpret_cast<const i4v*>(xl + 16 * ((4 * s + 2 * h + lo) ^ sw));
-            };
-            i4v h0 = rd(0, 0), l0 = rd(0, 1);
-            i4v h1 = SL > 1 ? rd(1, 0) : h0, l1 = SL > 1 ? rd(1, 1) : l0;
-#pragma unroll
-            for (int s = 0; s < SL; ++s) {
-                const bf8v ah = __builtin_bit_cast(bf8v, h0);
-                const bf8v al = __builtin_bit_cast(bf8v, l0);
-                h0 = h1;
-                l0 = l1;
-                if (s + 2 < SL) {
-                    h1 = rd(s + 2, 0);
-                    l1 = rd(s + 2, 1);
-                }
-                const int ks = part * SL + s;
-                hh = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, qh[ks], hh, 0, 0, 0);
-                hl = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, ql[ks], hl, 0, 0, 0);
-                lh = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, qh[ks], lh, 0, 0, 0);
-            }
-            // Schedule: each step's two LDS reads (for the step two ahead)
-            // between its three MFMAs.
-#pragma unroll
-            for (int s = 0; s < SL; ++s) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                if (s + 2 < SL) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                if (s + 2 < SL) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            }
-            // The previous tile's keys (its norms were published by the
-            // barrier of this tile's first slice), while the MFMAs run.
-            if (part == 0) offer(prev, t - 1);
+        for (int s = 0; s < NH; ++s) {
+            const int c = 4 * s + 2 * h;
+            const bf8v ah = __builtin_bit_cast(bf8v, *reinterpret_cast<const i4v*>(xl + 16 * (c ^ sw)));
+            const bf8v al = __builtin_bit_cast(bf8v, *reinterpret_cast<const i4v*>(xl + 16 * ((c + 1) ^ sw)));
+            hh = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, qh[s], hh, 0, 0, 0);
+            hl = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, ql[s], hl, 0, 0, 0);
+            lh = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, qh[s], lh, 0, 0, 0);
         }
-        prev = hh + (hl + lh);
+        const f16v part = hh + (hl + lh);
+        // Exchange and keys with the k half as a constant (kp is uniform
+        // over the wave, so this is a scalar branch).
+        if (kp == 0) exchange_and_offer(part, t, std::integral_constant<int, 0>());
+        else exchange_and_offer(part, t, std::integral_constant<int, 1>());
     }
-    __syncthreads();  // the last tile's norms
-    offer(prev, ntiles - 1);
     if (qvalid) {
-        uint64_t* out = ga.lists + (((size_t)qid * ga.nseg + seg) * 2 + h) * C;
+        uint64_t* out = ga.lists + (((size_t)qid * ga.nseg + seg) * kBf3Lists + 2 * kp + h) * C;
 #pragma unroll
         for (int i = 0; i < C; ++i) out[i] = lst[i];
     }
@@ -701,15 +701,15 @@ bool plan_gemm(int64_t n, int dim, int64_t nq, int kc, GemmPlan* out) {
 }
 
 size_t gemm_lists_bytes(const GemmPlan& p, int64_t nq) {
-    return (size_t)nq * (size_t)p.nseg * 2 * gemm_list_len(p.kc) * sizeof(uint64_t);
+    return (size_t)nq * (size_t)p.nseg * p.lps * gemm_list_len(p.kc) * sizeof(uint64_t);
 }
 
 // Unit roundoff for make_bounds that covers the split-bf16 dot error
-// g = 1.024 gamma_d(2^-23) + 3.01 2^-16 + 2^-22 (gamma_d(u_eff) = g).
+// g = 1.024 gamma_d(2^-23) + 3.01 2^-16 + 2^-21 (gamma_d(u_eff) = g).
 static double bf3_unit_roundoff(int dim) {
     const double u23 = 1.0 / 8388608.0;
     const double gd = dim * u23 / (1.0 - dim * u23);
-    const double g = 1.024 * gd + 3.01 / 65536.0 + 1.0 / 4194304.0;
+    const double g = 1.024 * gd + 3.01 / 65536.0 + 1.0 / 2097152.0;
     return g / ((double)dim * (1.0 + g));
 }
 
@@ -730,17 +730,18 @@ static void launch_bf3_dim_c(const GemmPlan& p, const uint32_t* split_rows, cons
         return true;
     }();
     (void)attr;
+    const dim3 block(64 * kBf3Waves);
     switch (metric) {
     case kMetricCosine:
-        hipLaunchKernelGGL((flat_gemm_bf16x3<DIM, kMetricCosine, C, BOUNDED>), grid, dim3(256), shmem,
+        hipLaunchKernelGGL((flat_gemm_bf16x3<DIM, kMetricCosine, C, BOUNDED>), grid, block, shmem,
                            s, split_rows, norms, n, split_q, queries, nq, bc, ga);
         break;
     case kMetricL2:
-        hipLaunchKernelGGL((flat_gemm_bf16x3<DIM, kMetricL2, C, BOUNDED>), grid, dim3(256), shmem, s,
+        hipLaunchKernelGGL((flat_gemm_bf16x3<DIM, kMetricL2, C, BOUNDED>), grid, block, shmem, s,
                            split_rows, norms, n, split_q, queries, nq, bc, ga);
         break;
     default:
-        hipLaunchKernelGGL((flat_gemm_bf16x3<DIM, kMetricIP, C, BOUNDED>), grid, dim3(256), shmem, s,
+        hipLaunchKernelGGL((flat_gemm_bf16x3<DIM, kMetricIP, C, BOUNDED>), grid, block, shmem, s,
                            split_rows, norms, n, split_q, queries, nq, bc, ga);
         break;
     }
@@ -789,7 +790,7 @@ hipError_t launch_flat_bf3(const GemmPlan& p, bool sampled, const uint32_t* spli
 
 hipError_t launch_bf3_bounds(const GemmPlan& p, int64_t nq, const uint64_t* lists, uint64_t* bound,
                              hipStream_t s) {
-    const int64_t per_query = (int64_t)p.s_nseg * 2 * gemm_list_len(p.kc);
+    const int64_t per_query = (int64_t)p.s_nseg * kBf3Lists * gemm_list_len(p.kc);
     hipLaunchKernelGGL(lists_kth_slot, dim3(1, (unsigned)nq), dim3(256),
                        sizeof(uint64_t) * 4 * (size_t)p.cap, s, p.kc, p.cap, per_query, lists, bound);
     return hipGetLastError();
@@ -836,7 +837,7 @@ static void launch_lists_merge(const GemmPlan& p, const float* rows, const float
                                const uint32_t* qbad, const FlatArgs& fa, hipStream_t s) {
     size_t shmem = sizeof(uint64_t) * 4 * (size_t)p.cap;
     hipLaunchKernelGGL(flat_lists_merge<NCH>, dim3(1, (unsigned)nq), dim3(256), shmem, s, rows,
-                       norms, n, dim, queries, metric, p.kc, p.cap, 2 * p.nseg,
+                       norms, n, dim, queries, metric, p.kc, p.cap, p.lps * p.nseg,
                        gemm_list_len(p.kc), lists, qbound, qbad, fa);
 }
 

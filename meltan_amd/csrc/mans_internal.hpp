@@ -45,6 +45,7 @@ struct GemmPlan {
     int nseg = 0;  // row segments, a multiple of 8
     int nqb = 0;   // blocks of 128 queries
     int64_t rows_per_seg = 0;
+    int lps = 2;   // lane lists per query and segment (4 on the split-bf16 path)
     // The split-bf16 path's bounding launch over sampled rows.
     int s_nseg = 0;
     int64_t s_rows_per_seg = 0;
