@@ -370,7 +370,7 @@ struct Bf3Shape {
 template <int DIM>
 size_t bf3_lds_bytes() {
     return kBf3Slots * (size_t)Bf3Shape<DIM>::TILE_BYTES +
-           sizeof(float) * (kBf3Waves * 64 * 8 + kBf3Slots * kGemmRows + 4 * kGemmRows);
+           sizeof(float) * (2 * kBf3Waves * 64 * 8 + kBf3Slots * kGemmRows + 4 * kGemmRows);
 }
 
 struct Bf3Args {
@@ -402,8 +402,8 @@ __global__ __launch_bounds__(512, 1) void flat_gemm_bf16x3(
     constexpr int NH = G::NH, CPR = G::CPR, SWZ = G::SWZ;
     extern __shared__ uint64_t lds[];
     uint8_t* ring = reinterpret_cast<uint8_t*>(lds);                      // [slot][half][32][CPR][16]
-    float* xch = reinterpret_cast<float*>(ring + kBf3Slots * G::TILE_BYTES);  // [wave][64][8]
-    float* tvn = xch + kBf3Waves * 64 * 8;   // [slot][32] raw vn
+    float* xch = reinterpret_cast<float*>(ring + kBf3Slots * G::TILE_BYTES);  // [2][wave][64][8]
+    float* tvn = xch + 2 * kBf3Waves * 64 * 8;  // [slot][32] raw vn
     float* tva = tvn + kBf3Slots * kGemmRows;  // [2][32] vn (NaN past the segment)
     float* tvb = tva + 2 * kGemmRows;          // [2][32] sqrt(vn), or 1 / sqrt(vn) for cosine
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -484,30 +484,33 @@ __global__ __launch_bounds__(512, 1) void flat_gemm_bf16x3(
         }
     };
 
-    // Sends the partner half the 8 sums it keys, receives the 8 this wave
-    // keys (rows 8 (v / 4) + 4 h + v % 4, v = 8 KP .. 8 KP + 7), adds them
-    // and offers the keys: branch-free, then the insertion path only for a
+    // Tile t's sums: the partner half's 8 (rows it keys) go to LDS buffer
+    // t & 1, this wave's 8 stay in `keep`.  After the next barrier the
+    // partner's 8 for this wave are read back, added (the same IEEE sum in
+    // either wave) and keyed: rows 8 (v / 4) + 4 h + v % 4 for
+    // v = 8 KP .. 8 KP + 7, branch-free, then the insertion path only for a
     // lane with a key at or below its threshold.
-    auto exchange_and_offer = [&](const f16v& part, int64_t t, auto kpc) {
+    auto send = [&](const f16v& part, int64_t t, float (&keep)[8], auto kpc) {
         constexpr int KP = decltype(kpc)::value;
         constexpr int other = 8 * (1 - KP), my0 = 8 * KP;
-        float* mine = xch + (wave * 64 + lane) * 8;
+        float* mine = xch + (((int)(t & 1) * kBf3Waves + wave) * 64 + lane) * 8;
         *reinterpret_cast<f4v*>(mine) = f4v{part[other], part[other + 1], part[other + 2], part[other + 3]};
         *reinterpret_cast<f4v*>(mine + 4) =
             f4v{part[other + 4], part[other + 5], part[other + 6], part[other + 7]};
-        // A barrier without the vector-memory wait of __syncthreads: the
-        // next tile's loads stay in flight.
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-        const float* theirs = xch + (((wave + 4) & 7) * 64 + lane) * 8;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) keep[i] = part[my0 + i];
+    };
+    auto receive_and_offer = [&](const float (&keep)[8], int64_t t, auto kpc) {
+        constexpr int KP = decltype(kpc)::value;
+        constexpr int my0 = 8 * KP;
+        const float* theirs = xch + (((int)(t & 1) * kBf3Waves + ((wave + 4) & 7)) * 64 + lane) * 8;
         const f4v r0 = *reinterpret_cast<const f4v*>(theirs);
         const f4v r1 = *reinterpret_cast<const f4v*>(theirs + 4);
         float f[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            f[i] = part[my0 + i] + r0[i];
-            f[4 + i] = part[my0 + 4 + i] + r1[i];
+            f[i] = keep[i] + r0[i];
+            f[4 + i] = keep[4 + i] + r1[i];
         }
         const int tb = (int)(t & 1) * kGemmRows;
         float key[8];
@@ -557,10 +560,13 @@ __global__ __launch_bounds__(512, 1) void flat_gemm_bf16x3(
     };
 
     issue(0);
+    float keep[8] = {};
     for (int64_t t = 0; t < ntiles; ++t) {
         // Tile t is in LDS once this wave's loads are done; the barrier
-        // publishes every wave's part and frees the other slot (tile t - 1).
+        // publishes every wave's part (and the previous tile's sums and
+        // norms) and frees the other slot (tile t - 1).
         wait_vmcnt<0>();
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         issue(t + 1);
@@ -589,10 +595,21 @@ __global__ __launch_bounds__(512, 1) void flat_gemm_bf16x3(
             lh = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, qh[s], lh, 0, 0, 0);
         }
         const f16v part = hh + (hl + lh);
-        // Exchange and keys with the k half as a constant (kp is uniform
-        // over the wave, so this is a scalar branch).
-        if (kp == 0) exchange_and_offer(part, t, std::integral_constant<int, 0>());
-        else exchange_and_offer(part, t, std::integral_constant<int, 1>());
+        // The k half as a constant (kp is uniform over the wave, so these
+        // are scalar branches): the previous tile's keys (its partner sums
+        // were published by this tile's barrier), then this tile's send.
+        if (kp == 0) {
+            if (t > 0) receive_and_offer(keep, t - 1, std::integral_constant<int, 0>());
+            send(part, t, keep, std::integral_constant<int, 0>());
+        } else {
+            if (t > 0) receive_and_offer(keep, t - 1, std::integral_constant<int, 1>());
+            send(part, t, keep, std::integral_constant<int, 1>());
+        }
+    }
+    if (ntiles > 0) {
+        __syncthreads();  // the last tile's partner sums and norms
+        if (kp == 0) receive_and_offer(keep, ntiles - 1, std::integral_constant<int, 0>());
+        else receive_and_offer(keep, ntiles - 1, std::integral_constant<int, 1>());
     }
     if (qvalid) {
         uint64_t* out = ga.lists + (((size_t)qid * ga.nseg + seg) * kBf3Lists + 2 * kp + h) * C;
