@@ -706,11 +706,11 @@ bool plan_gemm(int64_t n, int dim, int64_t nq, int kc, GemmPlan* out) {
     p.rows_per_seg = (rps + kGemmRows - 1) / kGemmRows * kGemmRows;
     p.nseg = (int)nseg;
     // Bounding launch of the split-bf16 contraction: up to 64 segments
-    // spread over the rows, about a sixteenth of the rows in all.
+    // spread over the rows, about a thirty-second of the rows in all.
     p.s_nseg = (int)std::min<int64_t>(nseg, 64);
     const int64_t srps = (n + p.s_nseg - 1) / p.s_nseg;
     p.s_rows_per_seg = (srps + kGemmRows - 1) / kGemmRows * kGemmRows;
-    int64_t srows = (n / 16 / p.s_nseg + kGemmRows - 1) / kGemmRows * kGemmRows;
+    int64_t srows = (n / 32 / p.s_nseg + kGemmRows - 1) / kGemmRows * kGemmRows;
     srows = std::max<int64_t>(srows, kGemmRows);
     p.s_seg_rows = std::min(srows, p.s_rows_per_seg);
     *out = p;
