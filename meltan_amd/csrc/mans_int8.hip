@@ -179,6 +179,18 @@ __device__ __forceinline__ int sum8(int v) {
     return v;
 }
 
+// Sampled bounds of the streaming scan.  A launch that scans the first
+// scan_rows rows of each block's range writes each block's smallest slot
+// to block_min_out ([query][block]) and stops; the kc-th smallest of a
+// query's block minima is its bound (kc blocks hold a sampled row at or
+// below it, so no row above it is among the kc smallest).  The full launch
+// then admits no key above it (qbound).
+struct I8ScanBounds {
+    int64_t scan_rows = INT64_MAX;
+    const uint64_t* qbound = nullptr;
+    uint64_t* block_min_out = nullptr;
+};
+
 struct Int8Planes {
     const int8_t* codes;
     const float* u;
@@ -196,7 +208,7 @@ __global__ __launch_bounds__(256) void int8_scan(
     Int8Planes pl, const float* __restrict__ rows, const float* __restrict__ norms, int64_t n,
     int dim, const float* __restrict__ queries, const uint32_t* __restrict__ qidx,
     const int8_t* __restrict__ qcodes, const Int8QueryCoef* __restrict__ coefs, int metric, int kc,
-    int cap, int64_t rows_per_block, int proof, FlatArgs fa) {
+    int cap, int64_t rows_per_block, int proof, FlatArgs fa, I8ScanBounds sb) {
     constexpr int NC8 = (NCH + 1) / 2;
     extern __shared__ uint64_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -215,8 +227,13 @@ __global__ __launch_bounds__(256) void int8_scan(
 
     WaveTopK sel;
     sel.init(lds + wave * cap, cap, kc);
+    // A query's bound: no row with a larger slot is among its kc smallest,
+    // so keys above its key are never admitted (ties at it are, which only
+    // adds rows the selection then orders by slot).
+    if (sb.qbound && sb.qbound[q] != kEmptySlot) sel.thresh = slot_key(sb.qbound[q]);
     const int64_t start = (int64_t)blockIdx.x * rows_per_block;
-    const int64_t end = start + rows_per_block < n ? start + rows_per_block : n;
+    const int64_t span = sb.scan_rows < rows_per_block ? sb.scan_rows : rows_per_block;
+    const int64_t end = start + span < n ? start + span : n;
     // Each 8-lane group takes kRows rows per step (rows g8 + 8 j of the
     // wave's 8 kRows), so a wave has 8 kRows rows of codes in flight.
     constexpr int kRows = 4;
@@ -268,6 +285,19 @@ __global__ __launch_bounds__(256) void int8_scan(
         sel.offer(vj, key, (uint32_t)rj);
     }
     sel.finish();
+    if (sb.block_min_out) {
+        // Sampled launch: the block's smallest slot (each wave's list is
+        // sorted, so its first slot is the wave's smallest).
+        __shared__ uint64_t wmin[4];
+        if (lane == 0) wmin[wave] = sel.buf[0];
+        __syncthreads();
+        if (tid == 0) {
+            uint64_t m = wmin[0];
+            for (int w = 1; w < (int)(blockDim.x >> 6); ++w) m = wmin[w] < m ? wmin[w] : m;
+            sb.block_min_out[(int64_t)q * gridDim.x + blockIdx.x] = m;
+        }
+        return;
+    }
     if (!flat_block_epilogue(sel, lds, cap, kc, fa)) return;
 
     const int lr = lane & 15, dim4 = dim >> 2;
@@ -286,11 +316,11 @@ static void launch_int8_scan(const FlatPlan& p, const Int8Planes& pl, const floa
                              const float* norms, int64_t n, int dim, const float* queries,
                              const uint32_t* qidx, int64_t nq, const int8_t* qcodes,
                              const Int8QueryCoef* coefs, int metric, int proof, const FlatArgs& fa,
-                             hipStream_t s) {
+                             const I8ScanBounds& sb, hipStream_t s) {
     size_t shmem = sizeof(uint64_t) * 4 * (size_t)p.cap;
     hipLaunchKernelGGL(int8_scan<NCH>, dim3(p.nblk, (unsigned)nq), dim3(256), shmem, s, pl, rows,
                        norms, n, dim, queries, qidx, qcodes, coefs, metric, p.kc, p.cap,
-                       p.rows_per_block, proof, fa);
+                       p.rows_per_block, proof, fa, sb);
 }
 
 // ---------------------------------------------------------------------------
@@ -600,6 +630,18 @@ __global__ __launch_bounds__(256) void int8_lists_bound(int kc, int cap, int nli
     if (threadIdx.x == 0) qbound[q] = lds[kc - 1];
 }
 
+// grid (1, nq): bound[q] = the kc-th smallest of the query's nblk block
+// minima from the sampled streaming launch (kEmptySlot when nblk < kc).
+__global__ __launch_bounds__(256) void int8_mins_bound(int kc, int cap, int nblk,
+                                                       const uint64_t* __restrict__ mins,
+                                                       uint64_t* __restrict__ bound) {
+    extern __shared__ uint64_t lds[];
+    const uint32_t q = blockIdx.y;
+    WaveTopK sel;
+    block_select_lists(mins + (size_t)q * nblk, (int64_t)nblk, lds, cap, kc, sel);
+    if (threadIdx.x == 0) bound[q] = lds[kc - 1];
+}
+
 static bool i8gemm_ks(int stride, int* ks) {
     const int k = (stride + 31) / 32;
     switch (k) {
@@ -791,6 +833,15 @@ static int int8_exact_fallback(mans_ctx* ctx, const mans_corpus* c, const float*
     return e == hipSuccess ? MANS_OK : hip_fail(e, "int8 fallback scatter");
 }
 
+// MANS_INT8_BOUNDS=0 turns the streaming scan's sampled bounds off.
+static bool int8_sampled_bounds() {
+    static const bool on = [] {
+        const char* e = std::getenv("MANS_INT8_BOUNDS");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+
 // Device queries and outputs; h_rounds (nullable, host) receives the rounds.
 static int int8_search_run(mans_ctx* ctx, mans_corpus* c, const float* d_q, int64_t nq, int64_t k,
                            uint32_t metric, int32_t mode, int64_t budget, float* d_dist,
@@ -882,16 +933,47 @@ static int int8_search_run(mans_ctx* ctx, mans_corpus* c, const float* d_q, int6
         fa.group_blocks = p.group_blocks;
         fa.ngroups = p.ngroups;
         if (timed) ctx->time_begin(slot, st);
-        switch (nch) {
-        case 1: launch_int8_scan<1>(p, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, proof, fa, st); break;
-        case 2: launch_int8_scan<2>(p, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, proof, fa, st); break;
-        case 3: launch_int8_scan<3>(p, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, proof, fa, st); break;
-        case 4: launch_int8_scan<4>(p, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, proof, fa, st); break;
-        case 6: launch_int8_scan<6>(p, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, proof, fa, st); break;
-        case 8: launch_int8_scan<8>(p, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, proof, fa, st); break;
-        default: return fail(MANS_PIPELINE_UNAVAILABLE, "int8 scan: unsupported dim");
+        auto launch = [&](const FlatPlan& p, const I8ScanBounds& sb) {
+            switch (nch) {
+            case 1: launch_int8_scan<1>(p, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, proof, fa, sb, st); break;
+            case 2: launch_int8_scan<2>(p, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, proof, fa, sb, st); break;
+            case 3: launch_int8_scan<3>(p, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, proof, fa, sb, st); break;
+            case 4: launch_int8_scan<4>(p, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, proof, fa, sb, st); break;
+            case 6: launch_int8_scan<6>(p, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, proof, fa, sb, st); break;
+            default: launch_int8_scan<8>(p, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, proof, fa, sb, st); break;
+            }
+            return hipGetLastError();
+        };
+        if (nch != 1 && nch != 2 && nch != 3 && nch != 4 && nch != 6 && nch != 8)
+            return fail(MANS_PIPELINE_UNAVAILABLE, "int8 scan: unsupported dim");
+        I8ScanBounds sb;
+        // Blocks of at least 256 rows: a launch over the first sixteenth of
+        // each block's rows gives every query its bound first.
+        if (idx.empty() && p.rows_per_block >= 256 && p.nblk >= kc && int8_sampled_bounds()) {
+            const size_t mins_bytes = (size_t)cnt * p.nblk * sizeof(uint64_t);
+            e = slot->bounds.ensure(mins_bytes + (size_t)nq * sizeof(uint64_t), ctx->fail_alloc);
+            if (e != hipSuccess) return hip_fail(e, "int8 scan bounds");
+            uint64_t* mins = (uint64_t*)slot->bounds.p;
+            uint64_t* qb = mins + (size_t)cnt * p.nblk;
+            // The sampled launch keeps one slot per wave (kc 1).
+            FlatPlan p1 = p;
+            p1.kc = 1;
+            p1.cap = flat_cap_for(1);
+            I8ScanBounds s0;
+            s0.scan_rows = (p.rows_per_block / 16 + 15) / 16 * 16;
+            s0.block_min_out = mins;
+            e = launch(p1, s0);
+            if (e == hipSuccess) {
+                // All queries run (no index map): launch row = query id.
+                const int bcap = flat_cap_for((int)kc);
+                hipLaunchKernelGGL(int8_mins_bound, dim3(1, (unsigned)cnt), dim3(256),
+                                   sizeof(uint64_t) * 4 * (size_t)bcap, st, (int)kc, bcap, p.nblk,
+                                   (const uint64_t*)mins, qb);
+                e = hipGetLastError();
+            }
+            sb.qbound = qb;
         }
-        e = hipGetLastError();
+        if (e == hipSuccess) e = launch(p, sb);
         ctx->time_end(slot, st, "int8_scan");
         if (e == hipSuccess)
             e = hipMemcpyAsync(slot->status_h.p, fb.status, (size_t)cnt, hipMemcpyDeviceToHost, st);

@@ -43,6 +43,7 @@ struct Slot {
     bool counters_dirty = false;  // a launch failed: re-zero the merge counters
     DevBuf aux0, aux1, aux2, aux3;
     DevBuf qsplit, qbad;          // split-bf16 queries and their range flags
+    DevBuf bounds;                // per-query bounds of the int8 streaming scan
     PinnedBuf status_h, stage_h, result_h;  // pinned status, query staging, results
     ~Slot();
 };
