@@ -851,24 +851,85 @@ __global__ __launch_bounds__(256) void ivfpq_scan(PqArgs pa, const float* __rest
         const float* cen = pa.coarse + (int64_t)probes[p] * pa.dim;
         for (int d = tid; d < pa.dim; d += 256) qres[d] = qp[d] - cen[d];
         __syncthreads();
-        for (int e = tid; e < pa.m * 256; e += 256) {
-            const int s = e >> 8;
-            lut[e] = simd_distance(qres + s * pa.dsub, pa.books + (int64_t)e * pa.dsub, pa.dsub,
-                                   pa.metric);
+        const uint32_t* crow = reinterpret_cast<const uint32_t*>(pa.codes + (seg[2 * p] + a) * pa.m);
+        // Codes of a row as 16-byte loads when m is a multiple of 16 (rows
+        // then start 16-byte aligned); the next 256 rows' codes load while
+        // the current ones are scored, and the first ones while the LUT is
+        // built.  The score adds the m entries in code order
+        // (IVFPQIndex.swift:418-452) either way.
+        const int m16 = (pa.m & 15) == 0 && pa.m <= 64 ? pa.m >> 4 : 0;
+        const int64_t nrow = b - a;
+        auto load_codes = [&](int64_t r, i4v (&c4)[4]) {
+            const uint32_t* cw = crow + (r < nrow ? r : 0) * mw;
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                c4[c] = c < m16 ? reinterpret_cast<const i4v*>(cw)[c] : i4v{0, 0, 0, 0};
+        };
+        i4v cur[4];
+        if (m16 > 0) load_codes(tid, cur);
+        const int lut_n = pa.m * 256;
+        if (pa.dsub == 2) {
+            // Two-dimensional subvectors: each thread's codebook entries are
+            // loaded in batches of 12 before any is used, so their latencies
+            // overlap (one load at a time would serialise 48 of them).
+            const float2* bk = reinterpret_cast<const float2*>(pa.books);
+            constexpr int kB = 12;
+            for (int e0 = tid; e0 < lut_n; e0 += 256 * kB) {
+                float2 bv[kB];
+#pragma unroll
+                for (int u = 0; u < kB; ++u) {
+                    const int e = e0 + 256 * u;
+                    bv[u] = e < lut_n ? bk[e] : make_float2(0.0f, 0.0f);
+                }
+#pragma unroll
+                for (int u = 0; u < kB; ++u) {
+                    const int e = e0 + 256 * u;
+                    if (e < lut_n) {
+                        const float bb[2] = {bv[u].x, bv[u].y};
+                        lut[e] = simd_distance(qres + 2 * (e >> 8), bb, 2, pa.metric);
+                    }
+                }
+            }
+        } else {
+            for (int e = tid; e < lut_n; e += 256) {
+                const int s = e >> 8;
+                lut[e] = simd_distance(qres + s * pa.dsub, pa.books + (int64_t)e * pa.dsub, pa.dsub,
+                                       pa.metric);
+            }
         }
         __syncthreads();
-        const uint32_t* crow = reinterpret_cast<const uint32_t*>(pa.codes + (seg[2 * p] + a) * pa.m);
-        for (int64_t base = 0; base < b - a; base += 256) {
+        for (int64_t base = 0; base < nrow; base += 256) {
             const int64_t r = base + tid;
-            const bool v = r < b - a;
+            const bool v = r < nrow;
             const uint32_t* cw = crow + (v ? r : 0) * mw;
             float score = 0.0f;
-            for (int w = 0; w < mw; ++w) {
-                const uint32_t word = cw[w];
-                score += lut[(4 * w + 0) * 256 + (word & 0xFF)];
-                score += lut[(4 * w + 1) * 256 + ((word >> 8) & 0xFF)];
-                score += lut[(4 * w + 2) * 256 + ((word >> 16) & 0xFF)];
-                score += lut[(4 * w + 3) * 256 + (word >> 24)];
+            if (m16 > 0) {
+                i4v c4[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) c4[c] = cur[c];
+                if (base + 256 < nrow) load_codes(r + 256, cur);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    if (c < m16) {
+#pragma unroll
+                        for (int w = 0; w < 4; ++w) {
+                            const uint32_t word = (uint32_t)c4[c][w];
+                            const int sb = 16 * c + 4 * w;
+                            score += lut[(sb + 0) * 256 + (word & 0xFF)];
+                            score += lut[(sb + 1) * 256 + ((word >> 8) & 0xFF)];
+                            score += lut[(sb + 2) * 256 + ((word >> 16) & 0xFF)];
+                            score += lut[(sb + 3) * 256 + (word >> 24)];
+                        }
+                    }
+                }
+            } else {
+                for (int w = 0; w < mw; ++w) {
+                    const uint32_t word = cw[w];
+                    score += lut[(4 * w + 0) * 256 + (word & 0xFF)];
+                    score += lut[(4 * w + 1) * 256 + ((word >> 8) & 0xFF)];
+                    score += lut[(4 * w + 2) * 256 + ((word >> 16) & 0xFF)];
+                    score += lut[(4 * w + 3) * 256 + (word >> 24)];
+                }
             }
             sel.offer(v, score, (uint32_t)(pre + a + r));
         }
