@@ -721,6 +721,43 @@ __device__ inline int sorted_list_replay(const float* in_score, const uint32_t* 
     return count;
 }
 
+// simd_distance with b read at stride bstride (centroids stored
+// dimension-major, so consecutive lanes read consecutive floats); the same
+// operations in the same order.
+__device__ __forceinline__ float simd_distance_strided(const float* a, const float* b, int d,
+                                                       int64_t bstride, int metric) {
+    if (metric == kMetricL2) {
+        float s = 0.0f;
+        for (int i = 0; i < d; ++i) {
+            const float t = a[i] - b[i * bstride];
+            s += t * t;
+        }
+        return s;
+    }
+    if (metric == kMetricIP) {
+        float dot = 0.0f;
+        for (int i = 0; i < d; ++i) dot += a[i] * b[i * bstride];
+        return -dot;
+    }
+    if (d <= 0) return 1.0f;
+    float dot = 0.0f, na = 0.0f, nb = 0.0f;
+    for (int i = 0; i < d; ++i) dot += a[i] * b[i * bstride];
+    for (int i = 0; i < d; ++i) na += a[i] * a[i];
+    for (int i = 0; i < d; ++i) nb += b[i * bstride] * b[i * bstride];
+    const float denom = sqrtf(na) * sqrtf(nb);
+    return denom < 1e-10f ? 1.0f : 1.0f - dot / denom;
+}
+
+// dst[d][c] = src[c][d] for a rows x cols matrix.
+__global__ void transpose_kernel(const float* __restrict__ src, int64_t rows, int cols,
+                                 float* __restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * cols) return;
+    const int64_t r = i / cols;
+    const int c = (int)(i - r * cols);
+    dst[(int64_t)c * rows + r] = src[i];
+}
+
 // Probe selection, one block per query (selectClosestCentroids,
 // IVFPQIndex.swift:484-512): the sequential distance to every centroid, the
 // np + 64 smallest by (distance, index), then the BoundedSortedList(np)
@@ -728,7 +765,7 @@ __device__ inline int sorted_list_replay(const float* in_score, const uint32_t* 
 // the boundary than the selection kept.  dynamic LDS: 4 * cap slots + dim
 // floats.
 __global__ __launch_bounds__(256) void pq_probes(const float* __restrict__ queries, int dim,
-                                                 const float* __restrict__ coarse, int nlist,
+                                                 const float* __restrict__ coarse_t, int nlist,
                                                  int metric, int np, int kc, int cap,
                                                  uint32_t* __restrict__ probes,
                                                  uint8_t* __restrict__ status) {
@@ -744,7 +781,7 @@ __global__ __launch_bounds__(256) void pq_probes(const float* __restrict__ queri
     for (int base = 0; base < nlist; base += blockDim.x) {
         const int c = base + tid;
         const bool v = c < nlist;
-        const float dist = v ? simd_distance(qs, coarse + (int64_t)c * dim, dim, metric) : 0.0f;
+        const float dist = v ? simd_distance_strided(qs, coarse_t + c, dim, nlist, metric) : 0.0f;
         sel.offer(v, dist, (uint32_t)c);
     }
     sel.finish();
@@ -1046,6 +1083,7 @@ struct mans_ivfpq {
     int64_t n = 0, dim = 0, nlist = 0, m = 0, dsub = 0;
     uint32_t metric = 0;
     mans::DevBuf coarse, books, offsets, list_ids, codes, assign;
+    mans::DevBuf coarse_t;  // centroids dimension-major ([dim][nlist]) for the probe scan
     std::vector<int64_t> h_offsets;
 };
 
@@ -1090,7 +1128,7 @@ static int ivfpq_search_run(mans_ctx* ctx, const mans_ivfpq* pq, const float* d_
     ctx->time_begin(slot, st);
     hipLaunchKernelGGL(pq_probes, dim3((unsigned)nq), dim3(256),
                        sizeof(uint64_t) * 4 * (size_t)pcap + sizeof(float) * dim, st, d_q, dim,
-                       (const float*)pq->coarse.p, (int)pq->nlist, (int)pq->metric, np, pkc, pcap,
+                       (const float*)pq->coarse_t.p, (int)pq->nlist, (int)pq->metric, np, pkc, pcap,
                        (uint32_t*)slot->aux1.p, (uint8_t*)slot->status.p);
     e = hipGetLastError();
     if (e == hipSuccess)
@@ -1386,6 +1424,13 @@ int mans_ivfpq_build(mans_ctx* ctx, const mans_corpus* corpus, const float* coar
     if (e == hipSuccess)
         e = hipMemcpyAsync(pq->books.p, codebooks, (size_t)m * 256 * pq->dsub * sizeof(float),
                            hipMemcpyHostToDevice, st);
+    if (e == hipSuccess) e = pq->coarse_t.ensure((size_t)nlist * dim * sizeof(float), ctx->fail_alloc);
+    if (e == hipSuccess && nlist > 0) {
+        const int64_t cells = nlist * dim;
+        hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)((cells + 255) / 256)), dim3(256), 0, st,
+                           (const float*)pq->coarse.p, nlist, (int)dim, (float*)pq->coarse_t.p);
+        e = hipGetLastError();
+    }
     if (e != hipSuccess) {
         delete pq;
         return hip_fail(e, "IVF-PQ upload");
