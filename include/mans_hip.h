@@ -58,6 +58,7 @@ extern "C" {
 #define MANS_RESOURCE_EXHAUSTED (-4)    /* ANNSError.gpuResourceExhausted (degradeable) */
 #define MANS_EXECUTION_FAILED (-5)      /* ANNSError.gpuExecutionFailed (degradeable) */
 #define MANS_SEARCH_FAILED (-6)         /* ANNSError.searchFailed (degradeable) */
+#define MANS_CORRUPT_FILE (-7)          /* ANNSError.corruptFile */
 
 #define MANS_METRIC_COSINE 0u
 #define MANS_METRIC_L2 1u
@@ -86,6 +87,35 @@ void mans_ctx_destroy(mans_ctx *ctx);
  * computed on the device in the scalar order of dots.c:40-47. */
 int mans_corpus_upload_f32(mans_ctx *ctx, const float *rows, int64_t n, int64_t dim,
                            mans_corpus **out);
+/* MANN v3 (mmap-compatible) index files, IndexSerializer.saveMmapCompatible
+ * (IndexSerializer.swift:74-140) and MmapIndexLoader.load
+ * (MmapIndexLoader.swift:38-196): a 28-byte little-endian header ("MANN",
+ * version 3, node count, degree, dim, metric code, storage type), then the
+ * vector, adjacency and distance sections each starting on a page boundary,
+ * then the trailer (IDMap byte count, IDMap JSON, entry point).  The page
+ * size is the writer's (getpagesize(); 16384 on Apple silicon): page_size 0
+ * means this host's.
+ *
+ * mans_mann_inspect validates a file as MmapIndexLoader.load does (magic,
+ * version, metric and storage codes, non-zero counts, section and trailer
+ * bounds, entry point below the node count; the IDMap JSON itself is not
+ * decoded) and fills `info`; MANS_CORRUPT_FILE with the reference's reason
+ * otherwise.  Needs no device. */
+typedef struct mans_mann_info {
+    uint32_t version, node_count, degree, dim, metric, storage_type, entry_point;
+    int64_t page_size;
+    int64_t vector_offset, vector_bytes, adjacency_offset, distance_offset, trailer_offset;
+    int64_t idmap_bytes;
+} mans_mann_info;
+int mans_mann_inspect(const char *path, int64_t page_size, mans_mann_info *info);
+/* The loadReadOnly(.mmap) path: maps the file read-only and uploads its
+ * vector section straight from the mapping into a new corpus (through
+ * pinned staging buffers, two copies in flight), then computes the norms.
+ * fp32 storage only (FlatGPUSearch.isEligible, FlatGPUSearch.swift:193-209):
+ * f16 and binary files give MANS_PIPELINE_UNAVAILABLE.  out_metric
+ * (nullable) receives the file's metric code. */
+int mans_corpus_upload_mann(mans_ctx *ctx, const char *path, int64_t page_size, mans_corpus **out,
+                            uint32_t *out_metric);
 /* In-place row writes: copies `count` rows starting at `first_row` and
  * refreshes every derived plane of those rows (norms, int8 codes), the
  * analogue of the VectorBuffer write hooks that invalidate the norm and code

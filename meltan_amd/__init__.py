@@ -33,6 +33,7 @@ PIPELINE_UNAVAILABLE = -3
 RESOURCE_EXHAUSTED = -4
 EXECUTION_FAILED = -5
 SEARCH_FAILED = -6
+CORRUPT_FILE = -7
 ERROR_NAMES = {
     -1: "deviceNotSupported",
     -2: "dimensionMismatch",
@@ -40,13 +41,14 @@ ERROR_NAMES = {
     -4: "gpuResourceExhausted",
     -5: "gpuExecutionFailed",
     -6: "searchFailed",
+    -7: "corruptFile",
 }
 DEGRADEABLE = {-3, -4, -5, -6}  # Errors.swift:21-31
 
 # Every symbol the header declares, in declaration order.
 EXPORTS = [
     "mans_last_error", "mans_ctx_create", "mans_ctx_destroy", "mans_corpus_upload_f32",
-    "mans_corpus_write_rows", "mans_corpus_invalidate", "mans_corpus_release",
+    "mans_mann_inspect", "mans_corpus_upload_mann", "mans_corpus_write_rows", "mans_corpus_invalidate", "mans_corpus_release",
     "mans_corpus_count", "mans_corpus_dim", "mans_flat_search", "mans_flat_search_device",
     "mans_int8_search", "mans_int8_search_device", "mans_int8_codes_download",
     "mans_ivf_flat_build", "mans_kmeans", "mans_ivf_flat_search", "mans_ivf_flat_search_device",
@@ -67,6 +69,15 @@ class ANNSError(RuntimeError):
     @property
     def is_tier_degradeable(self) -> bool:
         return self.code in DEGRADEABLE
+
+
+class MannInfo(C.Structure):
+    """mans_mann_info: the validated layout of a MANN v3 file."""
+    _fields_ = [(name, C.c_uint32) for name in
+                ("version", "node_count", "degree", "dim", "metric", "storage_type", "entry_point")] + \
+               [(name, C.c_int64) for name in
+                ("page_size", "vector_offset", "vector_bytes", "adjacency_offset", "distance_offset",
+                 "trailer_offset", "idmap_bytes")]
 
 
 _lib = None
@@ -93,6 +104,9 @@ def lib() -> C.CDLL:
         L.mans_ctx_destroy.argtypes = [_vp]
         L.mans_ctx_destroy.restype = None
         L.mans_corpus_upload_f32.argtypes = [_vp, _vp, _i64, _i64, C.POINTER(_vp)]
+        L.mans_mann_inspect.argtypes = [C.c_char_p, _i64, C.POINTER(MannInfo)]
+        L.mans_corpus_upload_mann.argtypes = [_vp, C.c_char_p, _i64, C.POINTER(_vp),
+                                              C.POINTER(_u32)]
         L.mans_corpus_write_rows.argtypes = [_vp, _i64, _vp, _i64]
         L.mans_corpus_invalidate.argtypes = [_vp]
         L.mans_corpus_release.argtypes = [_vp]
@@ -126,6 +140,13 @@ def lib() -> C.CDLL:
         L.mans_timing_reset.argtypes = [_vp]
         _lib = L
     return _lib
+
+
+def mann_inspect(path, page_size: int = 0) -> MannInfo:
+    """Validates a MANN v3 file (no device needed); raises ANNSError."""
+    info = MannInfo()
+    _check(lib().mans_mann_inspect(str(path).encode(), page_size, C.byref(info)))
+    return info
 
 
 def _check(rc: int) -> None:
@@ -184,6 +205,17 @@ class Context:
         _check(lib().mans_corpus_upload_f32(self.handle, _ptr(rows), rows.shape[0], rows.shape[1],
                                             C.byref(h)))
         return Corpus(self, h, rows.shape[0], rows.shape[1])
+
+    def upload_mann(self, path, page_size: int = 0) -> tuple["Corpus", int]:
+        """loadReadOnly(.mmap): the vector section of a MANN v3 file into a
+        new corpus; returns (corpus, metric code of the file)."""
+        h = _vp()
+        metric = _u32()
+        _check(lib().mans_corpus_upload_mann(self.handle, str(path).encode(), page_size, C.byref(h),
+                                             C.byref(metric)))
+        n = lib().mans_corpus_count(h)
+        dim = lib().mans_corpus_dim(h)
+        return Corpus(self, h, n, dim), metric.value
 
     # timing ---------------------------------------------------------------
     def timing(self, enable: bool) -> None:

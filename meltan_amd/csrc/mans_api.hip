@@ -9,6 +9,11 @@
 #include "mans_internal.hpp"
 #include "mans_runtime.hpp"
 
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
@@ -213,6 +218,174 @@ int mans_corpus_upload_f32(mans_ctx* ctx, const float* rows, int64_t n, int64_t 
         delete c;
         return hip_fail(e, "corpus upload");
     }
+    *out = c;
+    return MANS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// MANN v3 files (MmapIndexLoader.swift:38-196).
+
+static uint32_t read_le32(const uint8_t* p) {
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+// Offsets and lengths with overflow checks, as checkedAdd / alignedOffset.
+static bool add_ok(int64_t a, int64_t b, int64_t* out) { return !__builtin_add_overflow(a, b, out); }
+static bool mul_ok(int64_t a, int64_t b, int64_t* out) { return !__builtin_mul_overflow(a, b, out); }
+static bool align_up(int64_t v, int64_t a, int64_t* out) {
+    const int64_t r = v % a;
+    return r == 0 ? (*out = v, true) : add_ok(v, a - r, out);
+}
+
+// Validates the mapped bytes [base, base + len) as a MANN v3 file.
+static int mann_parse(const uint8_t* base, int64_t len, int64_t page, mans_mann_info* info) {
+    std::memset(info, 0, sizeof(*info));
+    info->page_size = page;
+    if (len < 4 || std::memcmp(base, "MANN", 4) != 0) return fail(MANS_CORRUPT_FILE, "Invalid file magic");
+    if (len < 28) return fail(MANS_CORRUPT_FILE, "Unexpected EOF");
+    info->version = read_le32(base + 4);
+    if (info->version != 3)
+        return fail(MANS_CORRUPT_FILE,
+                    "Mmap loader requires version 3, found " + std::to_string(info->version));
+    info->node_count = read_le32(base + 8);
+    info->degree = read_le32(base + 12);
+    info->dim = read_le32(base + 16);
+    info->metric = read_le32(base + 20);
+    if (info->metric > 3) return fail(MANS_CORRUPT_FILE, "Unsupported metric code");
+    info->storage_type = read_le32(base + 24);
+    if (info->node_count == 0) return fail(MANS_CORRUPT_FILE, "Node count must be greater than zero");
+    if (info->degree == 0) return fail(MANS_CORRUPT_FILE, "Degree must be greater than zero");
+    if (info->storage_type > 2)
+        return fail(MANS_CORRUPT_FILE, "Unsupported storage type " + std::to_string(info->storage_type));
+    if (info->dim == 0) return fail(MANS_CORRUPT_FILE, "Dimension must be greater than zero");
+    const int64_t n = info->node_count, deg = info->degree, dim = info->dim;
+    int64_t vbytes, edges, abytes, dbytes;
+    bool ok = true;
+    if (info->storage_type == 2) {
+        if (dim % 8 != 0) return fail(MANS_CORRUPT_FILE, "Binary index has dim not divisible by 8");
+        ok = mul_ok(n, dim / 8, &vbytes);
+    } else {
+        int64_t elems;
+        ok = mul_ok(n, dim, &elems) && mul_ok(elems, info->storage_type == 1 ? 2 : 4, &vbytes);
+    }
+    ok = ok && mul_ok(n, deg, &edges) && mul_ok(edges, 4, &abytes) && mul_ok(edges, 4, &dbytes);
+    int64_t voff, aoff, doff, toff, t, vlen, alen, dlen, vend, aend, dend, tend;
+    ok = ok && align_up(28, page, &voff) && add_ok(voff, vbytes, &t) && align_up(t, page, &aoff) &&
+         add_ok(aoff, abytes, &t) && align_up(t, page, &doff) && add_ok(doff, dbytes, &t) &&
+         align_up(t, page, &toff) && align_up(vbytes, page, &vlen) && align_up(abytes, page, &alen) &&
+         align_up(dbytes, page, &dlen) && add_ok(voff, vlen, &vend) && add_ok(aoff, alen, &aend) &&
+         add_ok(doff, dlen, &dend) && add_ok(toff, 4, &tend);
+    if (!ok) return fail(MANS_CORRUPT_FILE, "Integer overflow while computing serialized sizes");
+    if (vend > len || aend > len || dend > len || tend > len)
+        return fail(MANS_CORRUPT_FILE, "Mmap sections are truncated");
+    const int64_t idmap = read_le32(base + toff);
+    int64_t idend, epend;
+    if (!add_ok(tend, idmap, &idend) || !add_ok(idend, 4, &epend) || epend > len)
+        return fail(MANS_CORRUPT_FILE, "Truncated IDMap payload");
+    info->entry_point = read_le32(base + idend);
+    if ((int64_t)info->entry_point >= n) return fail(MANS_CORRUPT_FILE, "Entry point is out of bounds");
+    info->vector_offset = voff;
+    info->vector_bytes = vbytes;
+    info->adjacency_offset = aoff;
+    info->distance_offset = doff;
+    info->trailer_offset = toff;
+    info->idmap_bytes = idmap;
+    return MANS_OK;
+}
+
+// A read-only mapping of a whole file, unmapped on scope exit.
+struct FileMap {
+    int fd = -1;
+    const uint8_t* p = nullptr;
+    int64_t len = 0;
+    ~FileMap() {
+        if (p) munmap(const_cast<uint8_t*>(p), (size_t)len);
+        if (fd >= 0) close(fd);
+    }
+    int open_map(const char* path) {
+        fd = ::open(path, O_RDONLY | O_CLOEXEC);
+        if (fd < 0) return fail(MANS_CORRUPT_FILE, std::string("cannot open ") + path);
+        struct stat st;
+        if (fstat(fd, &st) != 0) return fail(MANS_CORRUPT_FILE, "cannot stat the file");
+        len = (int64_t)st.st_size;
+        if (len == 0) return fail(MANS_CORRUPT_FILE, "File is too small");
+        void* m = mmap(nullptr, (size_t)len, PROT_READ, MAP_PRIVATE, fd, 0);
+        if (m == MAP_FAILED) return fail(MANS_CORRUPT_FILE, "cannot map the file");
+        p = (const uint8_t*)m;
+        (void)madvise(m, (size_t)len, MADV_SEQUENTIAL);
+        return MANS_OK;
+    }
+};
+
+static int64_t host_page_size(int64_t page) {
+    if (page > 0) return page;
+    const long ps = sysconf(_SC_PAGESIZE);
+    return ps > 0 ? (int64_t)ps : 4096;
+}
+
+int mans_mann_inspect(const char* path, int64_t page_size, mans_mann_info* info) {
+    if (!path || !info) return fail(MANS_SEARCH_FAILED, "mans_mann_inspect: NULL argument");
+    FileMap fm;
+    int rc = fm.open_map(path);
+    if (rc != MANS_OK) return rc;
+    return mann_parse(fm.p, fm.len, host_page_size(page_size), info);
+}
+
+int mans_corpus_upload_mann(mans_ctx* ctx, const char* path, int64_t page_size, mans_corpus** out,
+                            uint32_t* out_metric) {
+    if (!ctx || !path || !out) return fail(MANS_SEARCH_FAILED, "mans_corpus_upload_mann: NULL argument");
+    *out = nullptr;
+    FileMap fm;
+    int rc = fm.open_map(path);
+    if (rc != MANS_OK) return rc;
+    mans_mann_info info;
+    rc = mann_parse(fm.p, fm.len, host_page_size(page_size), &info);
+    if (rc != MANS_OK) return rc;
+    if (info.storage_type != 0)
+        return fail(MANS_PIPELINE_UNAVAILABLE, "the device scan reads fp32 vector storage only");
+    const int64_t n = info.node_count, dim = info.dim;
+    if (dim > 8192) return fail(MANS_SEARCH_FAILED, "dim above 8192 is not supported");
+    DeviceGuard dg(ctx->device);
+    SlotLease lease(ctx);
+    if (!lease.slot) return fail(MANS_RESOURCE_EXHAUSTED, "could not create a HIP stream");
+    hipStream_t st = lease.slot->stream;
+    mans_corpus* c = new mans_corpus();
+    c->ctx = ctx;
+    c->n = n;
+    c->dim = dim;
+    const size_t bytes = (size_t)info.vector_bytes;
+    hipError_t e = c->rows.ensure(bytes, ctx->fail_alloc);
+    if (e == hipSuccess) e = c->norms.ensure((size_t)n * sizeof(float), ctx->fail_alloc);
+    // The vector section straight from the mapping, through two pinned
+    // staging buffers: the host fills one while the other is copied.
+    constexpr size_t kChunk = (size_t)32 << 20;
+    void* stage[2] = {nullptr, nullptr};
+    hipEvent_t done[2] = {nullptr, nullptr};
+    for (int i = 0; i < 2 && e == hipSuccess; ++i) {
+        e = hipHostMalloc(&stage[i], std::min(kChunk, bytes));
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&done[i], hipEventDisableTiming);
+    }
+    const uint8_t* src = fm.p + info.vector_offset;
+    for (size_t off = 0, i = 0; e == hipSuccess && off < bytes; off += kChunk, ++i) {
+        const size_t len = std::min(kChunk, bytes - off);
+        const int b = (int)(i & 1);
+        if (i >= 2) e = hipEventSynchronize(done[b]);  // the copy out of this buffer is done
+        if (e != hipSuccess) break;
+        std::memcpy(stage[b], src + off, len);
+        e = hipMemcpyAsync((uint8_t*)c->rows.p + off, stage[b], len, hipMemcpyHostToDevice, st);
+        if (e == hipSuccess) e = hipEventRecord(done[b], st);
+    }
+    if (e == hipSuccess) e = launch_row_norms((const float*)c->rows.p, n, (int)dim, (float*)c->norms.p, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    for (int i = 0; i < 2; ++i) {
+        if (done[i]) (void)hipEventDestroy(done[i]);
+        if (stage[i]) (void)hipHostFree(stage[i]);
+    }
+    if (e != hipSuccess) {
+        delete c;
+        return hip_fail(e, "MANN upload");
+    }
+    if (out_metric) *out_metric = info.metric;
     *out = c;
     return MANS_OK;
 }
