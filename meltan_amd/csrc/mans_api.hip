@@ -629,7 +629,9 @@ static int flat_search_chunk(mans_ctx* ctx, const mans_corpus* c, const float* d
             FlatBuffers fb;
             fb.out_dist = d_dist;
             fb.out_ids = d_ids;
-            fb.status = (uint8_t*)slot->status.p;
+            // The proof status goes straight to pinned host memory (read
+            // after the round's one synchronisation, no copy).
+            fb.status = (uint8_t*)slot->status_h.p;
             uint64_t* lists = (uint64_t*)slot->cand.p;
             uint64_t* qbound = bf3 ? lists + lbytes / sizeof(uint64_t) : nullptr;
             const uint32_t* qbad = bf3 ? (const uint32_t*)slot->qbad.p : nullptr;
@@ -678,20 +680,19 @@ static int flat_search_chunk(mans_ctx* ctx, const mans_corpus* c, const float* d
             if (e != hipSuccess) return hip_fail(e, "flat scan workspace");
             fb.out_dist = d_dist;
             fb.out_ids = d_ids;
+            fb.status = (uint8_t*)slot->status_h.p;
             ctx->time_begin(slot, st);
             e = launch_flat_search(p, exact, (const float*)c->rows.p, (const float*)c->norms.p, n,
                                    dim, d_q, d_qidx, npend, (int)metric, fb, keff, kstride, st);
             ctx->time_end(slot, st, "flat_scan");
         }
-        // Results (when the caller wants them on the host) and the proof
-        // status come back together: one synchronisation per round.
+        // Results (when the caller wants them on the host) come back with
+        // the round's one synchronisation; the proof status is already in
+        // pinned host memory.
         if (e == hipSuccess && h_dist)
             e = hipMemcpyAsync(h_dist, d_dist, obytes, hipMemcpyDeviceToHost, st);
         if (e == hipSuccess && h_ids)
             e = hipMemcpyAsync(h_ids, d_ids, obytes, hipMemcpyDeviceToHost, st);
-        if (e == hipSuccess)
-            e = hipMemcpyAsync(slot->status_h.p, slot->status.p, (size_t)npend,
-                               hipMemcpyDeviceToHost, st);
         if (e == hipSuccess) e = hipStreamSynchronize(st);
         if (e != hipSuccess) {
             slot->counters_dirty = true;
@@ -746,10 +747,12 @@ int mans_flat_search(mans_ctx* ctx, const mans_corpus* c, const float* queries, 
     if (e == hipSuccess) e = s->result_h.ensure(2 * obytes);
     if (e == hipSuccess) e = stage_to_device(s, s->queries.p, queries, qbytes);
     if (e != hipSuccess) return hip_fail(e, "flat scan staging");
+    // The kernels write the results straight into pinned host memory
+    // (device-accessible): no copies back, one synchronisation.
     float* hd = (float*)s->result_h.p;
     uint32_t* hi = (uint32_t*)((char*)s->result_h.p + obytes);
-    int rc = flat_search_run(ctx, c, (const float*)s->queries.p, nq, k, metric, (float*)s->dist.p,
-                             (uint32_t*)s->ids.p, s->stream, s, hd, hi);
+    int rc = flat_search_run(ctx, c, (const float*)s->queries.p, nq, k, metric, hd, hi, s->stream,
+                             s, nullptr, nullptr);
     if (rc != MANS_OK) return rc;
     std::memcpy(out_dist, hd, obytes);
     std::memcpy(out_ids, hi, obytes);

@@ -285,9 +285,13 @@ FlatPlan plan_flat(int64_t n, int64_t nq, int kc, int64_t target_blocks) {
     p.cap = flat_cap_for(kc);
     static const int64_t flat_target = [] {
         const char* e = std::getenv("MANS_FLAT_BLOCKS");
-        return e ? std::max<int64_t>(1, std::atoll(e)) : (int64_t)1024;
+        return e ? std::max<int64_t>(1, std::atoll(e)) : (int64_t)0;
     }();
-    const int64_t target = target_blocks > 0 ? target_blocks : flat_target;
+    // About 1024 blocks per launch for large corpora; for smaller ones about
+    // one block per 196 rows (at least 256), so a block's fixed costs
+    // (list, head, merge inputs) stay small next to its rows.
+    const int64_t auto_target = std::min<int64_t>(1024, std::max<int64_t>(256, n / 196));
+    const int64_t target = target_blocks > 0 ? target_blocks : (flat_target > 0 ? flat_target : auto_target);
     int64_t want_blocks = (target + nq - 1) / nq;
     int64_t max_blocks = (n + 63) / 64;
     if (want_blocks > max_blocks) want_blocks = max_blocks;
