@@ -252,6 +252,21 @@ __global__ __launch_bounds__(256) void ivf_scan(
         const int64_t b = hi - pre < len ? hi - pre : len;
         if (a >= b) continue;
         const int64_t start = seg[2 * p] + a, end = seg[2 * p] + b;  // packed rows
+        if constexpr (!EXACT) {
+            // The streaming scan's step: the next 16 rows' loads are in
+            // flight while the current ones are reduced and offered.
+            const int slot = wave * 4 + grp;
+            f4v ra[1][NCH], rb[1][NCH];
+            float va[1], vb[1];
+            scan_load<NCH, false, 1>(ia.packed, ia.packed_norms, dim, dim4, start, end, slot, lr, ra, va);
+            for (int64_t base = start; base < end; base += 32) {
+                scan_load<NCH, false, 1>(ia.packed, ia.packed_norms, dim, dim4, base + 16, end, slot, lr, rb, vb);
+                scan_offer<NCH, 1>(ra, va, qv, qn, metric, bc, base, end, slot, lr, sel);
+                scan_load<NCH, false, 1>(ia.packed, ia.packed_norms, dim, dim4, base + 32, end, slot, lr, ra, va);
+                scan_offer<NCH, 1>(rb, vb, qv, qn, metric, bc, base + 16, end, slot, lr, sel);
+            }
+            continue;
+        }
         for (int64_t base = start; base < end; base += 32) {
             const int64_t r0 = base + wave * 4 + grp;
             const int64_t r1 = r0 + 16;

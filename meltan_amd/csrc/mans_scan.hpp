@@ -41,6 +41,65 @@ __device__ __forceinline__ float lower_key(float f, float qn, float vn, int metr
     return metric == kMetricIP ? k_ip : (metric == kMetricL2 ? k_l2 : k_cos);
 }
 
+// Loads of the streaming pass: R rows per 16-lane group (rows base + 4 wave
+// + grp + 16 j), clamped to the block's last row and, past the row's end,
+// replaced by zeros, so that no branch separates the loads.  The scheduling
+// barrier keeps every load of the step ahead of the arithmetic that uses it.
+template <int NCH, bool FULL, int R>
+__device__ __forceinline__ void scan_load(const float* __restrict__ rows,
+                                          const float* __restrict__ norms, int dim, int dim4,
+                                          int64_t base, int64_t end, int slot, int lr,
+                                          f4v (&a)[R][NCH], float (&vn)[R]) {
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        const int64_t r = base + slot + 16 * j;
+        vn[j] = norms[r < end ? r : end - 1];
+    }
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        const int64_t r = base + slot + 16 * j;
+        const float* p = rows + (r < end ? r : end - 1) * dim;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const int idx = lr + 16 * c;
+            if (FULL) {
+                a[j][c] = load_stream(p + 4 * idx);
+            } else {
+                const bool in = idx < dim4;
+                const f4v t = load_stream(p + 4 * (in ? idx : dim4 - 1));
+                a[j][c] = in ? t : f4v{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// Fast dots (two accumulators per row), keys and offers of one step.
+template <int NCH, int R, class Sel>
+__device__ __forceinline__ void scan_offer(const f4v (&a)[R][NCH], const float (&vn)[R],
+                                           const f4v* qv, float qn, int metric, const BoundCoef& bc,
+                                           int64_t base, int64_t end, int slot, int lr, Sel& sel) {
+    float s[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        float x = 0.0f, y = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            float& t = (c & 1) ? y : x;
+            t = fmaf(a[j][c].x, qv[c].x, t);
+            t = fmaf(a[j][c].y, qv[c].y, t);
+            t = fmaf(a[j][c].z, qv[c].z, t);
+            t = fmaf(a[j][c].w, qv[c].w, t);
+        }
+        s[j] = row16_sum(x + y);
+    }
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        const int64_t r = base + slot + 16 * j;
+        sel.offer(lr == 0 && r < end, lower_key(s[j], qn, vn[j], metric, bc), (uint32_t)r);
+    }
+}
+
 // Per-launch outputs and merge bookkeeping (indexed by blockIdx.y).
 struct FlatArgs {
     uint64_t* cand;      // [nq][nblk][kc]  block lists
