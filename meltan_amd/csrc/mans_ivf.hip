@@ -389,8 +389,10 @@ static int ivf_search_run(mans_ctx* ctx, const mans_ivf* ivf, const float* d_q, 
         }
     }
 
-    // Work items: rows per item about 2048 items' worth of the batch's
-    // average work, at least 128; the launch covers the largest queries.
+    // Work items: rows per item about 512 items' worth of the batch's
+    // average work, at least 128 (fewer, longer items keep the per-item
+    // list, merge and rescore costs small); the launch covers the largest
+    // queries.
     const int64_t avg_rows = std::max<int64_t>(1, ivf->n * np / std::max<int64_t>(1, ivf->nlist));
     int64_t max_rows = 0;
     {
@@ -401,7 +403,7 @@ static int ivf_search_run(mans_ctx* ctx, const mans_ivf* ivf, const float* d_q, 
     }
     static const int64_t target_items = [] {
         const char* ev = std::getenv("MANS_IVF_BLOCKS");
-        return ev ? std::max<int64_t>(1, std::atoll(ev)) : (int64_t)2048;
+        return ev ? std::max<int64_t>(1, std::atoll(ev)) : (int64_t)512;
     }();
 
     const int keff = (int)std::min<int64_t>(std::min<int64_t>(k, MANS_MAX_TOP_K), ivf->n);
