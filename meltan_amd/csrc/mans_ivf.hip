@@ -1167,7 +1167,7 @@ static int ivfpq_search_run(mans_ctx* ctx, const mans_ivfpq* pq, const float* d_
     }
     static const int64_t target_items = [] {
         const char* ev = std::getenv("MANS_IVFPQ_BLOCKS");
-        return ev ? std::max<int64_t>(1, std::atoll(ev)) : (int64_t)2048;
+        return ev ? std::max<int64_t>(1, std::atoll(ev)) : (int64_t)512;
     }();
     int kc = (int)k_adc + 64;
     std::vector<uint32_t> pending;
