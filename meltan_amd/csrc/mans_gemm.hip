@@ -687,7 +687,7 @@ bool plan_gemm(int64_t n, int dim, int64_t nq, int kc, GemmPlan* out) {
     }();
     static const int64_t target = [] {
         const char* e = std::getenv("MANS_GEMM_BLOCKS");
-        return e ? std::max<int64_t>(8, std::atoll(e)) : (int64_t)1024;
+        return e ? std::max<int64_t>(8, std::atoll(e)) : (int64_t)512;
     }();
     if (!gemm_dim_supported(dim) || kc > kGemmMaxKc || nq < min_batch || n < kGemmMinRows)
         return false;

@@ -669,7 +669,7 @@ static bool plan_i8gemm(int64_t n, int stride, int64_t nq, int64_t kc, I8GemmPla
     }();
     static const int64_t target = [] {
         const char* e = std::getenv("MANS_I8GEMM_BLOCKS");
-        return e ? std::max<int64_t>(8, std::atoll(e)) : (int64_t)2048;
+        return e ? std::max<int64_t>(8, std::atoll(e)) : (int64_t)1024;
     }();
     I8GemmPlan p;
     if (!i8gemm_ks(stride, &p.ks) || kc > kI8GemmMaxKc || nq < min_batch) return false;
