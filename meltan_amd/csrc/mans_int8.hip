@@ -189,6 +189,10 @@ struct I8ScanBounds {
     int64_t scan_rows = INT64_MAX;
     const uint64_t* qbound = nullptr;
     uint64_t* block_min_out = nullptr;
+    // Sampled launch over every query: its last block per query writes the
+    // bound_kc-th smallest block minimum to qbound_out.
+    uint64_t* qbound_out = nullptr;
+    int bound_kc = 0;
 };
 
 struct Int8Planes {
@@ -200,7 +204,94 @@ struct Int8Planes {
     int stride;
 };
 
-// grid (nblk, nq_launch); block 256; dynamic LDS: 4 * cap slots.
+// The streaming pass of one block over rows [start, end): each 8-lane group
+// takes kI8StreamRows rows per step (rows base + 8 kI8StreamRows wave + g8
+// + 8 j), and
+// the next step's codes are loaded while the current step's are reduced and
+// keyed, so a wave has two steps of codes in flight.  Every lane calls
+// offer(valid, key, row) once per step: lane l8 = j < kI8StreamRows keys
+// row j.
+constexpr int kI8StreamRows = 4;
+template <int NC8, class Offer>
+__device__ __forceinline__ void int8_stream(const Int8Planes& pl, const i4v (&qc)[NC8], int metric,
+                                            const Int8QueryCoef& coef, int64_t start, int64_t end,
+                                            Offer&& offer) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g8 = lane >> 3, l8 = lane & 7;
+    const int nchunk = pl.stride >> 4;
+    constexpr int64_t kStep = 4 * 8 * kI8StreamRows;  // rows per block step
+    struct Step {
+        i4v a[kI8StreamRows][NC8];
+        float pu[kI8StreamRows], pw[kI8StreamRows], pn[kI8StreamRows];
+    };
+    auto load = [&](int64_t base, Step& st) {
+#pragma unroll
+        for (int j = 0; j < kI8StreamRows; ++j) {
+            const int64_t r = base + wave * 8 * kI8StreamRows + g8 + 8 * j;
+            // Plane values of clamped rows, so every load is unconditional.
+            const int64_t cr = r < end ? r : start;
+            st.pu[j] = pl.u[cr];
+            st.pw[j] = pl.w[cr];
+            st.pn[j] = metric == kMetricL2 ? pl.normsq[cr] : pl.invsqrt[cr];
+            // Chunks past the row's end re-read its last chunk; the query's
+            // codes there are zero, so they add nothing (and the load needs
+            // no branch).
+            const i4v* src = reinterpret_cast<const i4v*>(pl.codes + cr * pl.stride);
+#pragma unroll
+            for (int c = 0; c < NC8; ++c) {
+                const int idx = l8 + 8 * c;
+                st.a[j][c] = __builtin_nontemporal_load(src + (idx < nchunk ? idx : nchunk - 1));
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // Every lane of a group ends with the group's dot of each row.
+    auto consume = [&](int64_t base, const Step& st) {
+        int sj = 0;
+        float uj = 0.0f, wj = 0.0f, nj = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kI8StreamRows; ++j) {
+            int s = 0;
+#pragma unroll
+            for (int c = 0; c < NC8; ++c) s = dot16_i8(st.a[j][c], qc[c], s);
+            s = sum8(s);
+            const bool mine = l8 == j;
+            sj = mine ? s : sj;
+            uj = mine ? st.pu[j] : uj;
+            wj = mine ? st.pw[j] : wj;
+            nj = mine ? st.pn[j] : nj;
+        }
+        const int64_t rj = base + wave * 8 * kI8StreamRows + g8 + 8 * (l8 < kI8StreamRows ? l8 : 0);
+        const bool vj = l8 < kI8StreamRows && rj < end;
+        offer(vj, int8_key(metric, coef, (float)sj, uj, wj, nj, nj), (uint32_t)rj);
+    };
+    if (start >= end) return;
+    Step sa, sb;
+    load(start, sa);
+    for (int64_t base = start; base < end; base += 2 * kStep) {
+        load(base + kStep, sb);
+        consume(base, sa);
+        load(base + 2 * kStep, sa);
+        consume(base + kStep, sb);
+    }
+}
+
+// The query's codes as the B side of dot16_i8: lane l8 holds 16-byte chunks
+// l8 + 8 c (zero past the row's end).
+template <int NC8>
+__device__ __forceinline__ void int8_query_chunks(const int8_t* qcodes, uint32_t q, int stride,
+                                                  i4v (&qc)[NC8]) {
+    const int l8 = threadIdx.x & 7, nchunk = stride >> 4;
+#pragma unroll
+    for (int c = 0; c < NC8; ++c) {
+        const int idx = l8 + 8 * c;
+        qc[c] = idx < nchunk ? *reinterpret_cast<const i4v*>(qcodes + (int64_t)q * stride + 16 * idx)
+                             : i4v{0, 0, 0, 0};
+    }
+}
+
+// grid (nblk, nq_launch); block 256; dynamic LDS: 4 * cap slots (and, for a
+// sampled launch, at least nblk slots).
 // NCH: float4 chunks per lane for the rescore (16 lanes per row); the int8
 // rows use (NCH + 1) / 2 16-byte chunks per lane with 8 lanes per row.
 template <int NCH>
@@ -212,18 +303,10 @@ __global__ __launch_bounds__(256) void int8_scan(
     constexpr int NC8 = (NCH + 1) / 2;
     extern __shared__ uint64_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int g8 = lane >> 3, l8 = lane & 7;
     const uint32_t q = qidx ? qidx[blockIdx.y] : blockIdx.y;
-    const int nchunk = pl.stride >> 4;
     const Int8QueryCoef coef = coefs[q];
-
     i4v qc[NC8];
-#pragma unroll
-    for (int c = 0; c < NC8; ++c) {
-        const int idx = l8 + 8 * c;
-        qc[c] = idx < nchunk ? *reinterpret_cast<const i4v*>(qcodes + (int64_t)q * pl.stride + 16 * idx)
-                             : i4v{0, 0, 0, 0};
-    }
+    int8_query_chunks<NC8>(qcodes, q, pl.stride, qc);
 
     WaveTopK sel;
     sel.init(lds + wave * cap, cap, kc);
@@ -234,56 +317,8 @@ __global__ __launch_bounds__(256) void int8_scan(
     const int64_t start = (int64_t)blockIdx.x * rows_per_block;
     const int64_t span = sb.scan_rows < rows_per_block ? sb.scan_rows : rows_per_block;
     const int64_t end = start + span < n ? start + span : n;
-    // Each 8-lane group takes kRows rows per step (rows g8 + 8 j of the
-    // wave's 8 kRows), so a wave has 8 kRows rows of codes in flight.
-    constexpr int kRows = 4;
-    for (int64_t base = start; base < end; base += 4 * 8 * kRows) {
-        int64_t r[kRows];
-        bool v[kRows];
-        float pu[kRows], pw[kRows], pn[kRows];
-        i4v a[kRows][NC8];
-#pragma unroll
-        for (int j = 0; j < kRows; ++j) {
-            r[j] = base + wave * 8 * kRows + g8 + 8 * j;
-            v[j] = r[j] < end;
-            // Plane values of clamped rows, so every load is unconditional.
-            const int64_t cr = v[j] ? r[j] : start;
-            pu[j] = pl.u[cr];
-            pw[j] = pl.w[cr];
-            pn[j] = metric == kMetricL2 ? pl.normsq[cr] : pl.invsqrt[cr];
-            // Chunks past the row's end re-read its last chunk; the query's
-            // codes there are zero, so they add nothing (and the load needs
-            // no branch).
-            const i4v* src = reinterpret_cast<const i4v*>(pl.codes + cr * pl.stride);
-#pragma unroll
-            for (int c = 0; c < NC8; ++c) {
-                const int idx = l8 + 8 * c;
-                a[j][c] = __builtin_nontemporal_load(src + (idx < nchunk ? idx : nchunk - 1));
-            }
-        }
-        // Every lane of a group ends with the group's dot of each row; lane
-        // l8 = j < kRows then keys row j, so one offer covers the step.
-        int sj = 0;
-        float uj = 0.0f, wj = 0.0f, nj = 0.0f;
-        int64_t rj = 0;
-        bool vj = false;
-#pragma unroll
-        for (int j = 0; j < kRows; ++j) {
-            int s = 0;
-#pragma unroll
-            for (int c = 0; c < NC8; ++c) s = dot16_i8(a[j][c], qc[c], s);
-            s = sum8(s);
-            const bool mine = l8 == j;
-            sj = mine ? s : sj;
-            uj = mine ? pu[j] : uj;
-            wj = mine ? pw[j] : wj;
-            nj = mine ? pn[j] : nj;
-            rj = mine ? r[j] : rj;
-            vj = mine ? v[j] : vj;
-        }
-        const float key = int8_key(metric, coef, (float)sj, uj, wj, nj, nj);
-        sel.offer(vj, key, (uint32_t)rj);
-    }
+    int8_stream<NC8>(pl, qc, metric, coef, start, end,
+                     [&](bool v, float key, uint32_t r) { sel.offer(v, key, r); });
     sel.finish();
     if (sb.block_min_out) {
         // Sampled launch: the block's smallest slot (each wave's list is
@@ -291,11 +326,25 @@ __global__ __launch_bounds__(256) void int8_scan(
         __shared__ uint64_t wmin[4];
         if (lane == 0) wmin[wave] = sel.buf[0];
         __syncthreads();
+        uint64_t* mins = sb.block_min_out + (int64_t)blockIdx.y * gridDim.x;
         if (tid == 0) {
             uint64_t m = wmin[0];
             for (int w = 1; w < (int)(blockDim.x >> 6); ++w) m = wmin[w] < m ? wmin[w] : m;
-            sb.block_min_out[(int64_t)q * gridDim.x + blockIdx.x] = m;
+            store_shared_slot(&mins[blockIdx.x], m);
         }
+        if (!sb.qbound_out) return;
+        // The last block of the query: the bound_kc-th smallest block minimum
+        // (minima of distinct rows, so at least bound_kc rows have slots at
+        // or below it).
+        uint32_t* arrive = fa.counters + (int64_t)blockIdx.y * (fa.ngroups + 1);
+        if (!block_arrive_last(arrive, gridDim.x)) return;
+        if (tid == 0) __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int i = tid; i < (int)gridDim.x; i += blockDim.x) lds[i] = load_shared_slot(&mins[i]);
+        __syncthreads();
+        __shared__ uint32_t hist[256];
+        uint64_t kth;
+        block_radix_cut([&](int64_t i) { return lds[i]; }, gridDim.x, sb.bound_kc, hist, &kth);
+        if (tid == 0) sb.qbound_out[blockIdx.y] = kth;
         return;
     }
     if (!flat_block_epilogue(sel, lds, cap, kc, fa)) return;
@@ -318,9 +367,195 @@ static void launch_int8_scan(const FlatPlan& p, const Int8Planes& pl, const floa
                              const Int8QueryCoef* coefs, int metric, int proof, const FlatArgs& fa,
                              const I8ScanBounds& sb, hipStream_t s) {
     size_t shmem = sizeof(uint64_t) * 4 * (size_t)p.cap;
+    if (sb.block_min_out) shmem = std::max(shmem, sizeof(uint64_t) * (size_t)p.nblk);
     hipLaunchKernelGGL(int8_scan<NCH>, dim3(p.nblk, (unsigned)nq), dim3(256), shmem, s, pl, rows,
                        norms, n, dim, queries, qidx, qcodes, coefs, metric, p.kc, p.cap,
                        p.rows_per_block, proof, fa, sb);
+}
+
+// Threshold-collect scan (one query per grid row, every query of the
+// launch).  Every row whose slot is at or below the query's bound (the
+// kc-th smallest slot of a sample of rows, so the kc smallest slots of all
+// rows are among them) is gathered by its block, which rescores it exactly
+// (the dots.c order) and appends its slot and its exact (distance, id)
+// slot to the query's buffers.  The last block of the query selects the kc
+// smallest slots (radix select), sorts their exact slots and writes the
+// first k and the proof status.  A block with more than kCollectLdsSlots
+// such rows, or more than I8Collect::ccap of them in all, gives the status
+// kStatusReselect and nothing else is written (the caller selects again
+// with the lists).
+struct I8Collect {
+    const uint64_t* qbound;  // [nq]
+    uint64_t* cbuf;          // [nq][ccap] slots (int8 keys)
+    uint64_t* ebuf;          // [nq][ccap] exact (distance, id) slots
+    int64_t ccap;
+};
+constexpr int kCollectLdsSlots = 4096;  // rows gathered per block; candidates selected in LDS
+constexpr size_t kCollectShmem = sizeof(uint64_t) * (256 + kCollectLdsSlots);
+
+// grid (nblk, nq); block 256; dynamic LDS kCollectShmem; kc <= 256.
+template <int NCH>
+__global__ __launch_bounds__(256) void int8_collect(
+    Int8Planes pl, const float* __restrict__ rows, const float* __restrict__ norms, int64_t n,
+    int dim, const float* __restrict__ queries, const int8_t* __restrict__ qcodes,
+    const Int8QueryCoef* __restrict__ coefs, int metric, int kc, int64_t rows_per_block,
+    int proof, FlatArgs fa, I8Collect cl) {
+    constexpr int NC8 = (NCH + 1) / 2;
+    extern __shared__ uint64_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t q = blockIdx.y;
+    const Int8QueryCoef coef = coefs[q];
+    i4v qc[NC8];
+    int8_query_chunks<NC8>(qcodes, q, pl.stride, qc);
+    const uint64_t bound = cl.qbound[q];
+    uint32_t* arrive = fa.counters + (int64_t)q * (fa.ngroups + 1);
+    uint32_t* appended = arrive + 1;
+    uint64_t* cbuf = cl.cbuf + (int64_t)q * cl.ccap;
+    uint64_t* ebuf = cl.ebuf + (int64_t)q * cl.ccap;
+    const int64_t start = (int64_t)blockIdx.x * rows_per_block;
+    const int64_t end = start + rows_per_block < n ? start + rows_per_block : n;
+    uint64_t* top = lds;         // 256 slots (the last block's selection)
+    uint64_t* cand = lds + 256;  // kCollectLdsSlots slots
+    __shared__ uint32_t blk_count, blk_base;
+    if (tid == 0) blk_count = 0;
+    __syncthreads();
+    int8_stream<NC8>(pl, qc, metric, coef, start, end, [&](bool v, float key, uint32_t r) {
+        const uint64_t s = pack_slot(key, r);
+        const bool pass = v && s <= bound;
+        const uint64_t m = __ballot(pass);
+        if (m == 0) return;
+        const int leader = __ffsll((unsigned long long)m) - 1;
+        uint32_t base = 0;
+        if (lane == leader) base = atomicAdd(&blk_count, (uint32_t)__popcll(m));
+        base = (uint32_t)__shfl((int)base, leader);
+        const uint32_t pos = base + (uint32_t)__popcll(m & lanemask_lt());
+        if (pass && pos < (uint32_t)kCollectLdsSlots) cand[pos] = s;
+    });
+    __syncthreads();
+    const uint32_t nb = blk_count;
+    if (nb > (uint32_t)kCollectLdsSlots) {
+        // Too many rows for the block buffer: push the query's count past
+        // the capacity so that its last block reports kStatusReselect.
+        if (tid == 0)
+            __hip_atomic_fetch_add(appended, (uint32_t)cl.ccap + 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    } else if (nb > 0) {
+        if (tid == 0)
+            blk_base = __hip_atomic_fetch_add(appended, nb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // Exact rescore of the gathered rows: one row per 16-lane group
+        // (lane lr holds float4 chunks lr + 16 c of the row and the query).
+        const int lr = lane & 15, grp = wave * 4 + (lane >> 4), dim4 = dim >> 2;
+        const float* qp = queries + (int64_t)q * dim;
+        f4v qv[NCH];
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const int idx = lr + 16 * c;
+            qv[c] = idx < dim4 ? *reinterpret_cast<const f4v*>(qp + 4 * idx) : f4v{0.f, 0.f, 0.f, 0.f};
+        }
+        __syncthreads();
+        const int64_t gb = blk_base;
+        for (uint32_t i0 = 0; i0 < nb; i0 += 16) {
+            const uint32_t i = i0 + grp;
+            const bool valid = i < nb;
+            const uint64_t s = valid ? cand[i] : 0ull;
+            const uint32_t id = valid ? slot_id(s) : 0u;
+            f4v a[NCH];
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+                const int idx = lr + 16 * c;
+                a[c] = (valid && idx < dim4) ? *reinterpret_cast<const f4v*>(rows + (int64_t)id * dim + 4 * idx)
+                                             : f4v{0.f, 0.f, 0.f, 0.f};
+            }
+            const float dot = chain_dot<NCH>(a, qv, dim4);
+            if (valid && lr == 0 && gb + i < cl.ccap) {
+                const float dist = host_distance(dot, coef.qn, metric == kMetricIP ? 0.0f : norms[id], metric);
+                store_shared_slot(cbuf + gb + i, s);
+                store_shared_slot(ebuf + gb + i, pack_slot(dist, id));
+            }
+        }
+    }
+    if (!block_arrive_last(arrive, gridDim.x)) return;
+    __shared__ uint32_t s_total;
+    if (tid == 0) {
+        s_total = __hip_atomic_load(appended, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(appended, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    const int64_t total = s_total;
+    if (total > cl.ccap) {
+        if (tid == 0) fa.status[q] = kStatusReselect;
+        return;
+    }
+    __shared__ uint32_t hist[256];
+    __shared__ int ntop;
+    const bool in_lds = total <= kCollectLdsSlots;
+    if (in_lds)
+        for (int64_t i = tid; i < total; i += blockDim.x) cand[i] = load_shared_slot(cbuf + i);
+    if (tid == 0) ntop = 0;
+    __syncthreads();
+    auto get = [&](int64_t i) { return in_lds ? cand[i] : load_shared_slot(cbuf + i); };
+    uint64_t kth;
+    const uint64_t cut = block_radix_cut(get, total, kc, hist, &kth);
+    // The selected rows' exact slots, and the largest selected slot (the
+    // kc-th, or the last of fewer).
+    uint64_t mx = 0;
+    for (int64_t i = tid; i < total; i += blockDim.x) {
+        const uint64_t s = get(i);
+        if (s <= cut) {
+            const int p = atomicAdd(&ntop, 1);
+            if (p < 256) top[p] = load_shared_slot(ebuf + i);  // at most kc <= 256 (distinct slots)
+            mx = s > mx ? s : mx;
+        }
+    }
+    const uint64_t cut_key = block_reduce_u64<true>(mx);  // (its barriers order top[] too)
+    const int ncand = ntop < 256 ? ntop : 256;
+    int sort_n = 64;
+    while (sort_n < ncand) sort_n <<= 1;
+    for (int i = ncand + tid; i < sort_n; i += blockDim.x) top[i] = kEmptySlot;
+    __syncthreads();
+    if (tid < 64) wave_bitonic_sort(top, sort_n);
+    __syncthreads();
+    const int kout = fa.k < ncand ? fa.k : ncand;
+    for (int i = tid; i < fa.k_stride; i += blockDim.x) {
+        float dv = kFltMax;
+        uint32_t id = kEmptyId;
+        if (i < kout) {
+            id = slot_id(top[i]);
+            dv = slot_key(top[i]);
+        }
+        fa.out_dist[(int64_t)q * fa.k_stride + i] = dv;
+        fa.out_ids[(int64_t)q * fa.k_stride + i] = id;
+    }
+    if (tid == 0) {
+        const float cutoff = ncand > 0 ? slot_key(cut_key) : 0.0f;
+        const bool all_rows = (int64_t)ncand >= n;
+        bool ok;
+        if (proof == kProofNone) {
+            ok = true;
+        } else if (proof == kProofMargin) {
+            // BoundedExactScan.swift:108-113
+            const float tau = kout > 0 ? slot_key(top[kout - 1]) : 0.0f;
+            double margin = fabs((double)tau) * 1e-6;
+            margin = margin < 1e-7 ? 1e-7 : margin;
+            ok = all_rows || ncand < fa.k || (double)cutoff >= (double)tau + margin;
+        } else {
+            ok = all_rows || (kout > 0 && cutoff >= slot_key(top[kout - 1]));
+        }
+        fa.status[q] = ok ? 0 : 1;
+    }
+}
+
+template <int NCH>
+static hipError_t launch_int8_collect(const FlatPlan& p, const Int8Planes& pl, const float* rows,
+                                      const float* norms, int64_t n, int dim, const float* queries,
+                                      int64_t nq, const int8_t* qcodes, const Int8QueryCoef* coefs,
+                                      int metric, int kc, int proof, const FlatArgs& fa,
+                                      const I8Collect& cl, hipStream_t s) {
+    hipLaunchKernelGGL(int8_collect<NCH>, dim3(p.nblk, (unsigned)nq), dim3(256), kCollectShmem, s,
+                       pl, rows, norms, n, dim, queries, qcodes, coefs, metric, kc,
+                       p.rows_per_block, proof, fa, cl);
+    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
@@ -591,7 +826,6 @@ __global__ __launch_bounds__(256) void int8_lists_merge(
     const float* __restrict__ queries, int metric, int kc, int cap, int nlists,
     const uint64_t* __restrict__ lists, int proof, FlatArgs fa) {
     extern __shared__ uint64_t lds[];
-    __shared__ unsigned long long cut;
     const int lr = threadIdx.x & 15;
     const uint32_t q = blockIdx.y;
     const int dim4 = dim >> 2;
@@ -603,18 +837,16 @@ __global__ __launch_bounds__(256) void int8_lists_merge(
         qv[c] = idx < dim4 ? *reinterpret_cast<const f4v*>(qp + 4 * idx) : f4v{0.f, 0.f, 0.f, 0.f};
     }
     const uint64_t* lq = lists + (size_t)q * nlists * kI8List;
-    if (threadIdx.x == 0) cut = kEmptySlot;
-    __syncthreads();
-    unsigned long long mine = kEmptySlot;
+    uint64_t mine = kEmptySlot;
     for (int i = threadIdx.x; i < nlists; i += blockDim.x) {
         const uint64_t last = lq[(size_t)i * kI8List + kI8List - 1];
         mine = last < mine ? last : mine;  // a full list's largest slot
     }
-    atomicMin(&cut, mine);
+    const uint64_t cut = block_reduce_u64<false>(mine);
     WaveTopK sel;
     block_select_lists(lq, (int64_t)nlists * kI8List, lds, cap, kc, sel);  // ends in a barrier
     final_rescore_f4<NCH>(qv, rows, norms, n, dim, metric, q, lds, kc, fa, kFltMax, proof, nullptr,
-                          -1, (uint64_t)cut);
+                          -1, cut);
 }
 
 // grid (1, nq): each query's bound, the kc-th smallest slot of its lists
@@ -628,18 +860,6 @@ __global__ __launch_bounds__(256) void int8_lists_bound(int kc, int cap, int nli
     block_select_lists(lists + (size_t)q * nlists * kI8List, (int64_t)nlists * kI8List, lds, cap,
                        kc, sel);  // ends in a barrier
     if (threadIdx.x == 0) qbound[q] = lds[kc - 1];
-}
-
-// grid (1, nq): bound[q] = the kc-th smallest of the query's nblk block
-// minima from the sampled streaming launch (kEmptySlot when nblk < kc).
-__global__ __launch_bounds__(256) void int8_mins_bound(int kc, int cap, int nblk,
-                                                       const uint64_t* __restrict__ mins,
-                                                       uint64_t* __restrict__ bound) {
-    extern __shared__ uint64_t lds[];
-    const uint32_t q = blockIdx.y;
-    WaveTopK sel;
-    block_select_lists(mins + (size_t)q * nblk, (int64_t)nblk, lds, cap, kc, sel);
-    if (threadIdx.x == 0) bound[q] = lds[kc - 1];
 }
 
 static bool i8gemm_ks(int stride, int* ks) {
@@ -842,6 +1062,16 @@ static bool int8_sampled_bounds() {
     return on;
 }
 
+// The threshold-collect scan for single queries and small batches
+// (MANS_INT8_COLLECT=0 keeps the lists).
+static bool int8_collect_enabled() {
+    static const bool on = [] {
+        const char* e = std::getenv("MANS_INT8_COLLECT");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+
 // Device queries and outputs; h_rounds (nullable, host) receives the rounds.
 static int int8_search_run(mans_ctx* ctx, mans_corpus* c, const float* d_q, int64_t nq, int64_t k,
                            uint32_t metric, int32_t mode, int64_t budget, float* d_dist,
@@ -898,6 +1128,26 @@ static int int8_search_run(mans_ctx* ctx, mans_corpus* c, const float* d_q, int6
     const float* rows = (const float*)c->rows.p;
     const float* norms = (const float*)c->norms.p;
 
+    // The sampled launch over every query: the first sixteenth of each
+    // block's rows, one slot per wave; its last block per query writes the
+    // kc-th smallest block minimum, the query's bound, after the minima in
+    // slot->bounds.
+    auto sampled_bounds = [&](const FlatPlan& p, int64_t kc, int64_t cnt, auto&& launch) {
+        const size_t mins_bytes = (size_t)cnt * p.nblk * sizeof(uint64_t);
+        hipError_t e = slot->bounds.ensure(mins_bytes + (size_t)cnt * sizeof(uint64_t), ctx->fail_alloc);
+        if (e != hipSuccess) return e;
+        uint64_t* mins = (uint64_t*)slot->bounds.p;
+        FlatPlan p1 = p;
+        p1.kc = 1;
+        p1.cap = flat_cap_for(1);
+        I8ScanBounds s0;
+        s0.scan_rows = (p.rows_per_block / 16 + 15) / 16 * 16;
+        s0.block_min_out = mins;
+        s0.qbound_out = mins + (size_t)cnt * p.nblk;
+        s0.bound_kc = (int)kc;
+        return launch(p1, s0);
+    };
+
     // One streaming round over `idx` (empty: every query) at candidate count
     // kc; appends the queries whose proof failed to `grow`.
     auto stream_round = [&](const std::vector<uint32_t>& idx, int64_t kc, bool timed,
@@ -950,28 +1200,9 @@ static int int8_search_run(mans_ctx* ctx, mans_corpus* c, const float* d_q, int6
         // Blocks of at least 256 rows: a launch over the first sixteenth of
         // each block's rows gives every query its bound first.
         if (idx.empty() && p.rows_per_block >= 256 && p.nblk >= kc && int8_sampled_bounds()) {
-            const size_t mins_bytes = (size_t)cnt * p.nblk * sizeof(uint64_t);
-            e = slot->bounds.ensure(mins_bytes + (size_t)nq * sizeof(uint64_t), ctx->fail_alloc);
+            e = sampled_bounds(p, kc, cnt, launch);
             if (e != hipSuccess) return hip_fail(e, "int8 scan bounds");
-            uint64_t* mins = (uint64_t*)slot->bounds.p;
-            uint64_t* qb = mins + (size_t)cnt * p.nblk;
-            // The sampled launch keeps one slot per wave (kc 1).
-            FlatPlan p1 = p;
-            p1.kc = 1;
-            p1.cap = flat_cap_for(1);
-            I8ScanBounds s0;
-            s0.scan_rows = (p.rows_per_block / 16 + 15) / 16 * 16;
-            s0.block_min_out = mins;
-            e = launch(p1, s0);
-            if (e == hipSuccess) {
-                // All queries run (no index map): launch row = query id.
-                const int bcap = flat_cap_for((int)kc);
-                hipLaunchKernelGGL(int8_mins_bound, dim3(1, (unsigned)cnt), dim3(256),
-                                   sizeof(uint64_t) * 4 * (size_t)bcap, st, (int)kc, bcap, p.nblk,
-                                   (const uint64_t*)mins, qb);
-                e = hipGetLastError();
-            }
-            sb.qbound = qb;
+            sb.qbound = (const uint64_t*)slot->bounds.p + (size_t)cnt * p.nblk;
         }
         if (e == hipSuccess) e = launch(p, sb);
         ctx->time_end(slot, st, "int8_scan");
@@ -987,6 +1218,97 @@ static int int8_search_run(mans_ctx* ctx, mans_corpus* c, const float* d_q, int6
             const uint32_t qi = idx.empty() ? (uint32_t)i : idx[i];
             rounds[qi] += 1;
             if (sh[i]) grow.push_back(qi);
+        }
+        return MANS_OK;
+    };
+
+    // Streaming rounds over every query at kc <= 256 take the threshold-
+    // collect scan when the sampled bound applies: blocks of at least 256
+    // rows, at least kc blocks per query.
+    static const int64_t collect_target = [] {
+        const char* e = std::getenv("MANS_INT8_BLOCKS");
+        return e ? std::max<int64_t>(1, std::atoll(e)) : (int64_t)512;
+    }();
+    auto collect_plan = [&](int64_t kc, FlatPlan* p) {
+        if (kc > 256 || !int8_collect_enabled() || !int8_sampled_bounds()) return false;
+        *p = plan_flat(n, 1, (int)kc, collect_target);
+        return p->rows_per_block >= 256 && p->nblk >= kc;
+    };
+    // One threshold-collect round over every query at candidate count kc;
+    // queries whose bound let more rows through than the candidate buffer
+    // holds repeat the round with the lists.
+    auto collect_round = [&](const FlatPlan& p, int64_t kc, std::vector<uint32_t>& grow) -> int {
+        FlatBuffers fb;
+        hipError_t e = prepare_flat_buffers(ctx, slot, p, nq, st, &fb);
+        // Candidate buffers: slots, then exact slots, ccap = nblk kc each.
+        const int64_t ccap = (int64_t)p.nblk * p.kc;
+        if (e == hipSuccess)
+            e = slot->cand.ensure((size_t)nq * 2 * ccap * sizeof(uint64_t), ctx->fail_alloc);
+        fb.cand = (uint64_t*)slot->cand.p;
+        if (e == hipSuccess) e = slot->status_h.ensure((size_t)nq);
+        if (e != hipSuccess) return hip_fail(e, "int8 scan workspace");
+        FlatArgs fa = {};
+        fa.cand = fb.cand;
+        fa.gcand = fb.gcand;
+        fa.counters = fb.counters;
+        fa.out_dist = d_dist;
+        fa.out_ids = d_ids;
+        fa.status = (uint8_t*)slot->status_h.p;  // pinned: read after the stream syncs
+        fa.k = keff;
+        fa.k_stride = (int)k;
+        fa.group_blocks = p.group_blocks;
+        fa.ngroups = p.ngroups;
+        auto launch = [&](const FlatPlan& lp, const I8ScanBounds& sb) {
+            switch (nch) {
+            case 1: launch_int8_scan<1>(lp, pl, rows, norms, n, dim, d_q, nullptr, nq, qcodes, coefs, (int)metric, proof, fa, sb, st); break;
+            case 2: launch_int8_scan<2>(lp, pl, rows, norms, n, dim, d_q, nullptr, nq, qcodes, coefs, (int)metric, proof, fa, sb, st); break;
+            case 3: launch_int8_scan<3>(lp, pl, rows, norms, n, dim, d_q, nullptr, nq, qcodes, coefs, (int)metric, proof, fa, sb, st); break;
+            case 4: launch_int8_scan<4>(lp, pl, rows, norms, n, dim, d_q, nullptr, nq, qcodes, coefs, (int)metric, proof, fa, sb, st); break;
+            case 6: launch_int8_scan<6>(lp, pl, rows, norms, n, dim, d_q, nullptr, nq, qcodes, coefs, (int)metric, proof, fa, sb, st); break;
+            default: launch_int8_scan<8>(lp, pl, rows, norms, n, dim, d_q, nullptr, nq, qcodes, coefs, (int)metric, proof, fa, sb, st); break;
+            }
+            return hipGetLastError();
+        };
+        ctx->time_begin(slot, st);
+        e = sampled_bounds(p, kc, nq, launch);
+        ctx->time_end(slot, st, "int8_bound");
+        I8Collect cl;
+        cl.qbound = (const uint64_t*)slot->bounds.p + (size_t)nq * p.nblk;
+        cl.cbuf = fb.cand;
+        cl.ebuf = fb.cand + (size_t)nq * ccap;
+        cl.ccap = ccap;
+        ctx->time_begin(slot, st);
+        if (e == hipSuccess) {
+            switch (nch) {
+            case 1: e = launch_int8_collect<1>(p, pl, rows, norms, n, dim, d_q, nq, qcodes, coefs, (int)metric, (int)kc, proof, fa, cl, st); break;
+            case 2: e = launch_int8_collect<2>(p, pl, rows, norms, n, dim, d_q, nq, qcodes, coefs, (int)metric, (int)kc, proof, fa, cl, st); break;
+            case 3: e = launch_int8_collect<3>(p, pl, rows, norms, n, dim, d_q, nq, qcodes, coefs, (int)metric, (int)kc, proof, fa, cl, st); break;
+            case 4: e = launch_int8_collect<4>(p, pl, rows, norms, n, dim, d_q, nq, qcodes, coefs, (int)metric, (int)kc, proof, fa, cl, st); break;
+            case 6: e = launch_int8_collect<6>(p, pl, rows, norms, n, dim, d_q, nq, qcodes, coefs, (int)metric, (int)kc, proof, fa, cl, st); break;
+            default: e = launch_int8_collect<8>(p, pl, rows, norms, n, dim, d_q, nq, qcodes, coefs, (int)metric, (int)kc, proof, fa, cl, st); break;
+            }
+        }
+        ctx->time_end(slot, st, "int8_scan");
+        if (e == hipSuccess) e = hipStreamSynchronize(st);
+        if (e != hipSuccess) {
+            slot->counters_dirty = true;
+            return hip_fail(e, "int8 scan");
+        }
+        std::vector<uint32_t> redo;
+        const uint8_t* sh = (const uint8_t*)slot->status_h.p;
+        for (int64_t i = 0; i < nq; ++i) {
+            if (sh[i] == kStatusReselect) {
+                redo.push_back((uint32_t)i);
+                continue;
+            }
+            rounds[i] += 1;
+            if (sh[i]) grow.push_back((uint32_t)i);
+        }
+        ctx->reselects += (int64_t)redo.size();
+        if (!redo.empty()) {
+            int rc = stream_round(redo, kc, true, grow);
+            if (rc != MANS_OK) return rc;
+            std::sort(grow.begin(), grow.end());
         }
         return MANS_OK;
     };
@@ -1079,7 +1401,9 @@ static int int8_search_run(mans_ctx* ctx, mans_corpus* c, const float* d_q, int6
         std::vector<uint32_t> next;
         I8GemmPlan gp;
         int rc;
+        FlatPlan cp;
         if (first && plan_i8gemm(n, stride, nq, kc, &gp)) rc = gemm_round(gp, kc, next);
+        else if (pending.empty() && collect_plan(kc, &cp)) rc = collect_round(cp, kc, next);
         else rc = stream_round(pending, kc, !first, next);
         if (rc != MANS_OK) return rc;
         first = false;
