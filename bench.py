@@ -268,7 +268,7 @@ def bench_int8(args, ctx):
     corpus = ctx.upload(db)
     norms = oracle.row_norms(db)
     planes = oracle.int8_build(db)
-    gd, gi, _ = corpus.int8_search(q[:2], k, metric, mode=1, budget=budget)   # streaming scan
+    gd, gi, _ = corpus.int8_search(q[:2], k, metric, mode=1, budget=budget)   # threshold collect
     bd, bi, _ = corpus.int8_search(q[:64], k, metric, mode=1, budget=budget)  # i8 MFMA batch
     for i in range(2):
         od, oi, _ = oracle.int8_search(db, norms, planes, q[i], k, metric, mode=1, budget=budget)
@@ -289,9 +289,12 @@ def bench_int8(args, ctx):
         elapsed = timed(step, steps, 2, hip)
         kt = kernel_avg(ctx, step, min(steps, 10), ["int8_scan", "int8_bound", "int8_gemm", "int8_merge"], hip)
         if b == 1:
+            # The collect launch streams every row's codes and planes once;
+            # the bound launch before it reads a sixteenth of them.
             avg, launches = kt["int8_scan"]
             per = b * min(steps, 10) // max(launches, 1)
-            roof = roofline_hbm("int8_scan<6>", f"int8_{n}x{dim}_b{b}", per * n * (dim + 12), avg)
+            roof = roofline_hbm("int8_collect<6>", f"int8_{n}x{dim}_b{b}", per * n * (dim + 12), avg)
+            roof["bound_pass_us"] = round(kt["int8_bound"][0] * 1e6, 2) if kt["int8_bound"][1] else None
         else:
             # The batch is a 1024 x 1e6 x 384 int8 contraction on i8 MFMA
             # (dense peak 5.0 POP/s) with the key epilogue fused into it.
