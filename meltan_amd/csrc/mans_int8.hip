@@ -90,16 +90,15 @@ __global__ __launch_bounds__(256) void int8_build_codes(
     }
 }
 
-// One block per query (BoundedExactScan.swift:52-94).  dynamic LDS: dim floats.
-__global__ __launch_bounds__(256) void int8_query_prep(const float* __restrict__ queries, int dim,
-                                                       int stride, int8_t* __restrict__ qcodes,
-                                                       Int8QueryCoef* __restrict__ coefs) {
-    extern __shared__ float qsh[];
+// The query quantisation of BoundedExactScan.swift:52-94 by one block:
+// its codes (stride bytes, zero past dim) to `codes`, its coefficients to
+// *coef (written by thread 0: visible to the block after a barrier).  qsh:
+// dim floats of LDS, 16-byte aligned (overwritten); dim % 4 == 0.
+__device__ __forceinline__ void int8_prep_block(const float* __restrict__ qp, int dim, int stride,
+                                                float* qsh, int8_t* codes, Int8QueryCoef* coef) {
     __shared__ uint32_t max_bits;
     __shared__ int abs_sum;
     const int tid = threadIdx.x;
-    const int64_t q = blockIdx.x;
-    const float* qp = queries + q * dim;
     if (tid == 0) {
         max_bits = 0u;
         abs_sum = 0;
@@ -124,15 +123,26 @@ __global__ __launch_bounds__(256) void int8_query_prep(const float* __restrict__
             c = (int)(scaled >= 0.0 ? scaled + 0.5 : scaled - 0.5);
             c = c > 127 ? 127 : (c < -127 ? -127 : c);
         }
-        qcodes[q * stride + d] = (int8_t)c;
+        codes[d] = (int8_t)c;
         a += c < 0 ? -c : c;
     }
     atomicAdd(&abs_sum, a);
     __syncthreads();
+    // The squares in parallel (each rounded, as in the sequential loop),
+    // then thread 0's running sum over them in order.
+    for (int d = tid; d < dim; d += blockDim.x) qsh[d] = qsh[d] * qsh[d];
+    __syncthreads();
     if (tid == 0) {
         float qn = 0.0f;  // the sequential norm of FlatGPUSearch.swift:532-535
-#pragma unroll 16
-        for (int d = 0; d < dim; ++d) qn += qsh[d] * qsh[d];
+        const f4v* sq = reinterpret_cast<const f4v*>(qsh);
+#pragma unroll 8
+        for (int i = 0; i < (dim >> 2); ++i) {
+            const f4v v = sq[i];
+            qn = qn + v.x;
+            qn = qn + v.y;
+            qn = qn + v.z;
+            qn = qn + v.w;
+        }
         const float qs = (float)qscale;
         const float qabs_half = (float)abs_sum / 2.0f;
         const float inv = qn > 1e-20f ? 1.0f / sqrtf(qn) : 0.0f;
@@ -144,8 +154,17 @@ __global__ __launch_bounds__(256) void int8_query_prep(const float* __restrict__
         c.qn = qn;
         c.pad = 0.0f;
         c.qn_d = (double)qn;
-        coefs[q] = c;
+        *coef = c;
     }
+}
+
+// One block per query.  dynamic LDS: dim floats.
+__global__ __launch_bounds__(256) void int8_query_prep(const float* __restrict__ queries, int dim,
+                                                       int stride, int8_t* __restrict__ qcodes,
+                                                       Int8QueryCoef* __restrict__ coefs) {
+    extern __shared__ float qsh[];
+    const int64_t q = blockIdx.x;
+    int8_prep_block(queries + q * dim, dim, stride, qsh, qcodes + q * stride, coefs + q);
 }
 
 // Lower-bound key of one row, BoundedExactScan.swift:178-228, in the
@@ -193,7 +212,12 @@ struct I8ScanBounds {
     // bound_kc-th smallest block minimum to qbound_out.
     uint64_t* qbound_out = nullptr;
     int bound_kc = 0;
+    // Non-null: the launch quantises the queries itself (dim <= kI8MaxDim)
+    // and stores the codes and coefficients here.
+    int8_t* prep_codes_out = nullptr;
+    Int8QueryCoef* prep_coefs_out = nullptr;
 };
+constexpr int kI8MaxDim = 512;  // NCH <= 8: 16 lanes x 8 float4 chunks
 
 struct Int8Planes {
     const int8_t* codes;
@@ -304,9 +328,27 @@ __global__ __launch_bounds__(256) void int8_scan(
     extern __shared__ uint64_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t q = qidx ? qidx[blockIdx.y] : blockIdx.y;
-    const Int8QueryCoef coef = coefs[q];
+    Int8QueryCoef coef;
     i4v qc[NC8];
-    int8_query_chunks<NC8>(qcodes, q, pl.stride, qc);
+    if (sb.prep_codes_out) {
+        // Sampled launch that also quantises the query (in every block;
+        // block 0 stores the codes and coefficients for later launches).
+        __shared__ __align__(16) float prep_q[kI8MaxDim];
+        __shared__ __align__(16) int8_t prep_codes[kI8MaxDim];
+        __shared__ Int8QueryCoef prep_coef;
+        int8_prep_block(queries + (int64_t)q * dim, dim, pl.stride, prep_q, prep_codes, &prep_coef);
+        __syncthreads();
+        coef = prep_coef;
+        int8_query_chunks<NC8>(prep_codes, 0, pl.stride, qc);
+        if (blockIdx.x == 0) {
+            for (int i = tid; i < pl.stride; i += blockDim.x)
+                sb.prep_codes_out[(int64_t)q * pl.stride + i] = prep_codes[i];
+            if (tid == 0) sb.prep_coefs_out[q] = prep_coef;
+        }
+    } else {
+        coef = coefs[q];
+        int8_query_chunks<NC8>(qcodes, q, pl.stride, qc);
+    }
 
     WaveTopK sel;
     sel.init(lds + wave * cap, cap, kc);
@@ -1108,11 +1150,15 @@ static int int8_search_run(mans_ctx* ctx, mans_corpus* c, const float* d_q, int6
     if (e != hipSuccess) return hip_fail(e, "int8 query workspace");
     int8_t* qcodes = (int8_t*)slot->aux0.p;
     Int8QueryCoef* coefs = (Int8QueryCoef*)slot->aux1.p;
-    ctx->time_begin(slot, st);
-    hipLaunchKernelGGL(int8_query_prep, dim3((unsigned)nq), dim3(256), sizeof(float) * dim, st, d_q,
-                       dim, stride, qcodes, coefs);
-    e = hipGetLastError();
-    if (e != hipSuccess) return hip_fail(e, "int8 query prep");
+    // The query quantisation: its own launch, or (a first round on the
+    // collect path) inside the sampled launch.
+    bool prep_done = false;
+    auto launch_prep = [&]() -> hipError_t {
+        prep_done = true;
+        hipLaunchKernelGGL(int8_query_prep, dim3((unsigned)nq), dim3(256), sizeof(float) * dim, st,
+                           d_q, dim, stride, qcodes, coefs);
+        return hipGetLastError();
+    };
 
     Int8Planes pl;
     pl.codes = (const int8_t*)c->i8_codes.p;
@@ -1132,7 +1178,8 @@ static int int8_search_run(mans_ctx* ctx, mans_corpus* c, const float* d_q, int6
     // block's rows, one slot per wave; its last block per query writes the
     // kc-th smallest block minimum, the query's bound, after the minima in
     // slot->bounds.
-    auto sampled_bounds = [&](const FlatPlan& p, int64_t kc, int64_t cnt, auto&& launch) {
+    auto sampled_bounds = [&](const FlatPlan& p, int64_t kc, int64_t cnt, auto&& launch,
+                              bool prep = false) {
         const size_t mins_bytes = (size_t)cnt * p.nblk * sizeof(uint64_t);
         hipError_t e = slot->bounds.ensure(mins_bytes + (size_t)cnt * sizeof(uint64_t), ctx->fail_alloc);
         if (e != hipSuccess) return e;
@@ -1145,6 +1192,10 @@ static int int8_search_run(mans_ctx* ctx, mans_corpus* c, const float* d_q, int6
         s0.block_min_out = mins;
         s0.qbound_out = mins + (size_t)cnt * p.nblk;
         s0.bound_kc = (int)kc;
+        if (prep) {
+            s0.prep_codes_out = qcodes;
+            s0.prep_coefs_out = coefs;
+        }
         return launch(p1, s0);
     };
 
@@ -1270,7 +1321,10 @@ static int int8_search_run(mans_ctx* ctx, mans_corpus* c, const float* d_q, int6
             return hipGetLastError();
         };
         ctx->time_begin(slot, st);
-        e = sampled_bounds(p, kc, nq, launch);
+        const bool prep = !prep_done && dim <= kI8MaxDim;
+        if (!prep_done && !prep) e = launch_prep();
+        if (e == hipSuccess) e = sampled_bounds(p, kc, nq, launch, prep);
+        prep_done = true;
         ctx->time_end(slot, st, "int8_bound");
         I8Collect cl;
         cl.qbound = (const uint64_t*)slot->bounds.p + (size_t)nq * p.nblk;
@@ -1402,8 +1456,14 @@ static int int8_search_run(mans_ctx* ctx, mans_corpus* c, const float* d_q, int6
         I8GemmPlan gp;
         int rc;
         FlatPlan cp;
-        if (first && plan_i8gemm(n, stride, nq, kc, &gp)) rc = gemm_round(gp, kc, next);
-        else if (pending.empty() && collect_plan(kc, &cp)) rc = collect_round(cp, kc, next);
+        const bool gemm = first && plan_i8gemm(n, stride, nq, kc, &gp);
+        const bool collect = !gemm && pending.empty() && collect_plan(kc, &cp);
+        if (!prep_done && !collect) {
+            e = launch_prep();
+            if (e != hipSuccess) return hip_fail(e, "int8 query prep");
+        }
+        if (gemm) rc = gemm_round(gp, kc, next);
+        else if (collect) rc = collect_round(cp, kc, next);
         else rc = stream_round(pending, kc, !first, next);
         if (rc != MANS_OK) return rc;
         first = false;
