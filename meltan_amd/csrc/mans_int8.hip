@@ -862,33 +862,57 @@ __global__ __launch_bounds__(256) void int8_gemm(Int8Planes pl, int64_t n,
 // 2 nseg lists, then the exact rescore in the dots.c order and the proof
 // (or none) of the streaming int8 scan; the status is kStatusReselect when
 // the lists cannot show the selection is the kc smallest.
+constexpr int kMergeLdsSlots = 4096;  // list slots selected in LDS (else read from memory)
+
 template <int NCH>
 __global__ __launch_bounds__(256) void int8_lists_merge(
     const float* __restrict__ rows, const float* __restrict__ norms, int64_t n, int dim,
-    const float* __restrict__ queries, int metric, int kc, int cap, int nlists,
-    const uint64_t* __restrict__ lists, int proof, FlatArgs fa) {
+    const float* __restrict__ queries, const Int8QueryCoef* __restrict__ coefs, int metric, int kc,
+    int nlists, const uint64_t* __restrict__ lists, int proof, FlatArgs fa) {
     extern __shared__ uint64_t lds[];
-    const int lr = threadIdx.x & 15;
+    const int tid = threadIdx.x;
     const uint32_t q = blockIdx.y;
-    const int dim4 = dim >> 2;
-    const float* qp = queries + (int64_t)q * dim;
-    f4v qv[NCH];
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-        const int idx = lr + 16 * c;
-        qv[c] = idx < dim4 ? *reinterpret_cast<const f4v*>(qp + 4 * idx) : f4v{0.f, 0.f, 0.f, 0.f};
-    }
     const uint64_t* lq = lists + (size_t)q * nlists * kI8List;
+    const int64_t total = (int64_t)nlists * kI8List;
+    uint64_t* top = lds;         // 256 slots
+    uint64_t* res = lds + 256;   // 256 slots
+    uint64_t* cand = lds + 512;  // the lists' slots, then the rescore stage
     uint64_t mine = kEmptySlot;
-    for (int i = threadIdx.x; i < nlists; i += blockDim.x) {
+    for (int i = tid; i < nlists; i += blockDim.x) {
         const uint64_t last = lq[(size_t)i * kI8List + kI8List - 1];
         mine = last < mine ? last : mine;  // a full list's largest slot
     }
     const uint64_t cut = block_reduce_u64<false>(mine);
-    WaveTopK sel;
-    block_select_lists(lq, (int64_t)nlists * kI8List, lds, cap, kc, sel);  // ends in a barrier
-    final_rescore_f4<NCH>(qv, rows, norms, n, dim, metric, q, lds, kc, fa, kFltMax, proof, nullptr,
-                          -1, cut);
+    const bool in_lds = total <= kMergeLdsSlots;
+    if (in_lds)
+        for (int64_t i = tid; i < total; i += blockDim.x) cand[i] = lq[i];
+    __shared__ uint32_t hist[256];
+    __shared__ int ntop;
+    if (tid == 0) ntop = 0;
+    __syncthreads();
+    // The kc smallest slots (the empty slots of lists that are not full
+    // are the largest values and are never taken).
+    auto get = [&](int64_t i) { return in_lds ? cand[i] : lq[i]; };
+    uint64_t kth;
+    const uint64_t sel = block_radix_cut(get, total, kc, hist, &kth);
+    for (int64_t i = tid; i < total; i += blockDim.x) {
+        const uint64_t s = get(i);
+        if (s != kEmptySlot && s <= sel) {
+            const int p = atomicAdd(&ntop, 1);
+            if (p < 256) top[p] = s;
+        }
+    }
+    __syncthreads();
+    const int ncand = ntop < kc ? ntop : kc;
+    prefetch_rows(rows, top, ncand, dim, res);
+    int sort_n = 64;
+    while (sort_n < kc) sort_n <<= 1;
+    for (int i = ncand + tid; i < sort_n; i += blockDim.x) top[i] = kEmptySlot;
+    __syncthreads();
+    if (tid < 64) wave_bitonic_sort(top, sort_n);
+    __syncthreads();
+    final_rescore_wide(queries + (int64_t)q * dim, coefs[q].qn, rows, norms, n, dim, metric, q, top,
+                       ncand, kc, res, reinterpret_cast<float*>(cand), fa, proof, cut);
 }
 
 // grid (1, nq): each query's bound, the kc-th smallest slot of its lists
@@ -1005,12 +1029,16 @@ static hipError_t launch_i8gemm(const I8GemmPlan& p, const Int8Planes& pl, int64
 
 template <int NCH>
 static void launch_i8_merge(const I8GemmPlan& p, const float* rows, const float* norms, int64_t n,
-                            int dim, const float* queries, int64_t nq, int metric, int kc,
-                            const uint64_t* lists, int proof, const FlatArgs& fa, hipStream_t s) {
-    const int cap = flat_cap_for(kc);
-    const size_t shmem = sizeof(uint64_t) * 4 * (size_t)cap;
+                            int dim, const float* queries, const Int8QueryCoef* coefs, int64_t nq,
+                            int metric, int kc, const uint64_t* lists, int proof, const FlatArgs& fa,
+                            hipStream_t s) {
+    const int64_t total = (int64_t)2 * p.nseg * kI8List;
+    const size_t m = (size_t)(kc + 63) / 64;
+    const size_t stage = sizeof(float) * 2 * 64 * m * kWideStride;
+    const size_t slots = total <= kMergeLdsSlots ? sizeof(uint64_t) * (size_t)total : 0;
+    const size_t shmem = sizeof(uint64_t) * 512 + std::max(stage, slots);
     hipLaunchKernelGGL(int8_lists_merge<NCH>, dim3(1, (unsigned)nq), dim3(256), shmem, s, rows,
-                       norms, n, dim, queries, metric, kc, cap, 2 * p.nseg, lists, proof, fa);
+                       norms, n, dim, queries, coefs, metric, kc, 2 * p.nseg, lists, proof, fa);
 }
 
 // Copies `count` rows of `width` floats: dst[i] = src[idx[i]].
@@ -1402,12 +1430,12 @@ static int int8_search_run(mans_ctx* ctx, mans_corpus* c, const float* d_q, int6
         ctx->time_begin(slot, st);
         if (e == hipSuccess) {
             switch (nch) {
-            case 1: launch_i8_merge<1>(gp, rows, norms, n, dim, d_q, nq, (int)metric, (int)kc, lists, proof, fa, st); break;
-            case 2: launch_i8_merge<2>(gp, rows, norms, n, dim, d_q, nq, (int)metric, (int)kc, lists, proof, fa, st); break;
-            case 3: launch_i8_merge<3>(gp, rows, norms, n, dim, d_q, nq, (int)metric, (int)kc, lists, proof, fa, st); break;
-            case 4: launch_i8_merge<4>(gp, rows, norms, n, dim, d_q, nq, (int)metric, (int)kc, lists, proof, fa, st); break;
-            case 6: launch_i8_merge<6>(gp, rows, norms, n, dim, d_q, nq, (int)metric, (int)kc, lists, proof, fa, st); break;
-            case 8: launch_i8_merge<8>(gp, rows, norms, n, dim, d_q, nq, (int)metric, (int)kc, lists, proof, fa, st); break;
+            case 1: launch_i8_merge<1>(gp, rows, norms, n, dim, d_q, coefs, nq, (int)metric, (int)kc, lists, proof, fa, st); break;
+            case 2: launch_i8_merge<2>(gp, rows, norms, n, dim, d_q, coefs, nq, (int)metric, (int)kc, lists, proof, fa, st); break;
+            case 3: launch_i8_merge<3>(gp, rows, norms, n, dim, d_q, coefs, nq, (int)metric, (int)kc, lists, proof, fa, st); break;
+            case 4: launch_i8_merge<4>(gp, rows, norms, n, dim, d_q, coefs, nq, (int)metric, (int)kc, lists, proof, fa, st); break;
+            case 6: launch_i8_merge<6>(gp, rows, norms, n, dim, d_q, coefs, nq, (int)metric, (int)kc, lists, proof, fa, st); break;
+            case 8: launch_i8_merge<8>(gp, rows, norms, n, dim, d_q, coefs, nq, (int)metric, (int)kc, lists, proof, fa, st); break;
             default: return fail(MANS_PIPELINE_UNAVAILABLE, "int8 scan: unsupported dim");
             }
             e = hipGetLastError();

@@ -748,4 +748,157 @@ __device__ __forceinline__ uint64_t block_radix_cut(Get&& get, int64_t total, in
     return cut;
 }
 
+// Starts bringing the candidate rows (ids in top[0, ncand)) into the L2
+// without holding registers: one 4-byte global-to-LDS load per 128-byte
+// line, each wave's into the same 256 bytes of `sink` (contents unused;
+// the loads are complete once a later load of the same thread is).
+__device__ __forceinline__ void prefetch_rows(const float* __restrict__ rows, const uint64_t* top,
+                                              int ncand, int dim, void* sink) {
+    const int lines = (dim * 4 + 127) / 128;
+    const int total = ncand * lines;
+    for (int i = threadIdx.x; i < total; i += blockDim.x) {
+        const int r = i / lines, l = i - r * lines;
+        const float* p = rows + (int64_t)slot_id(top[r]) * dim + 32 * l;
+        __builtin_amdgcn_global_load_lds(p, (__attribute__((address_space(3))) void*)sink, 4, 0, 0);
+    }
+}
+
+// Exact rescore of up to 64 M (<= blockDim.x = 256) candidates (ascending
+// in top[0, ncand)), one candidate per thread: thread t runs candidate t's
+// whole dot product in the dots.c order.  The rows reach LDS in pieces of
+// kWidePiece floats, loaded by the whole block (W pieces in flight, M
+// float4 loads per thread and piece) and written one piece ahead of the
+// threads that read them.  qp: the query (read with scalar loads); qn: its
+// sequential q.q.  res: 256 slots (it may be the sink of prefetch_rows);
+// stage: 2 * 64 M * kWideStride floats.  Outputs, proof and sel_cut as
+// final_rescore_f4 (status at blockIdx.y).  dim % 4 == 0.
+constexpr int kWidePiece = 16;
+constexpr int kWideStride = 20;  // floats per staged row piece (bank spread)
+template <int M, int W>
+__device__ __forceinline__ void final_rescore_wide_mw(const float* __restrict__ qp, float qn,
+                                                      const float* __restrict__ rows,
+                                                      const float* __restrict__ norms, int64_t n,
+                                                      int dim, int metric, uint32_t q,
+                                                      const uint64_t* top, int ncand, int kc,
+                                                      uint64_t* res, float* stage, const FlatArgs& fa,
+                                                      int proof, uint64_t sel_cut) {
+    const int tid = threadIdx.x;
+    const int npieces = (dim + kWidePiece - 1) / kWidePiece;
+    const int lr = tid >> 2, u = tid & 3;  // stages float4 u of rows lr + 64 m
+    const float* rp[M];
+    bool rv[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const int c = lr + 64 * m;
+        rv[m] = c < ncand;
+        rp[m] = rows + (int64_t)(rv[m] ? slot_id(top[c]) : 0u) * dim;
+    }
+    auto load_piece = [&](int pc, f4v (&v)[M]) {
+        const int off = kWidePiece * pc + 4 * u;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const bool in = rv[m] && off < dim;
+            const f4v t = *reinterpret_cast<const f4v*>(rp[m] + (in ? off : 0));
+            v[m] = in ? t : f4v{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    f4v v[W][M];
+#pragma unroll
+    for (int w = 0; w < W; ++w)
+        if (w < npieces) load_piece(w, v[w]);
+    float acc = 0.0f;
+    for (int pc0 = 0; pc0 < npieces; pc0 += W) {
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            const int pc = pc0 + w;
+            if (pc >= npieces) break;
+            float* buf = stage + (pc & 1) * 64 * M * kWideStride;
+#pragma unroll
+            for (int m = 0; m < M; ++m)
+                *reinterpret_cast<f4v*>(buf + (lr + 64 * m) * kWideStride + 4 * u) = v[w][m];
+            if (pc + W < npieces) load_piece(pc + W, v[w]);
+            __syncthreads();
+            if (tid < ncand) {
+                const float* xr = buf + tid * kWideStride;
+                const float* yr = qp + kWidePiece * pc;  // uniform: scalar loads
+                const int rem = dim - kWidePiece * pc;
+#pragma unroll
+                for (int i = 0; i < kWidePiece / 4; ++i) {
+                    if (4 * i >= rem) break;
+                    const f4v x = *reinterpret_cast<const f4v*>(xr + 4 * i);
+                    const f4v y = *reinterpret_cast<const f4v*>(yr + 4 * i);
+                    acc = acc + x.x * y.x;
+                    acc = acc + x.y * y.y;
+                    acc = acc + x.z * y.z;
+                    acc = acc + x.w * y.w;
+                }
+            }
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // prefetches into res have landed
+    __syncthreads();
+    int sort_n = 64;
+    while (sort_n < ncand) sort_n <<= 1;
+    if (tid < sort_n) {
+        uint64_t rs = kEmptySlot;
+        if (tid < ncand) {
+            const uint32_t cid = slot_id(top[tid]);
+            rs = pack_slot(host_distance(acc, qn, metric == kMetricIP ? 0.0f : norms[cid], metric),
+                           cid);
+        }
+        res[tid] = rs;
+    }
+    __syncthreads();
+    if (tid < 64) wave_bitonic_sort(res, sort_n);
+    __syncthreads();
+    const int kout = fa.k < ncand ? fa.k : ncand;
+    for (int i = tid; i < fa.k_stride; i += blockDim.x) {
+        float dv = kFltMax;
+        uint32_t id = kEmptyId;
+        if (i < kout) {
+            id = slot_id(res[i]);
+            dv = slot_key(res[i]);
+        }
+        fa.out_dist[(int64_t)q * fa.k_stride + i] = dv;
+        fa.out_ids[(int64_t)q * fa.k_stride + i] = id;
+    }
+    if (tid == 0) {
+        const float cutoff = ncand > 0 ? slot_key(top[ncand - 1]) : 0.0f;
+        const bool all_rows = (int64_t)ncand >= n;
+        bool ok;
+        if (proof == kProofNone) {
+            ok = true;
+        } else if (proof == kProofMargin) {
+            const float tau = kout > 0 ? slot_key(res[kout - 1]) : 0.0f;
+            double margin = fabs((double)tau) * 1e-6;
+            margin = margin < 1e-7 ? 1e-7 : margin;
+            ok = all_rows || ncand < fa.k || (double)cutoff >= (double)tau + margin;
+        } else {
+            ok = all_rows || (kout > 0 && cutoff >= slot_key(res[kout - 1]));
+        }
+        const bool sel_exact = sel_cut == kEmptySlot || (ncand == kc && top[kc - 1] <= sel_cut);
+        fa.status[blockIdx.y] = !sel_exact ? kStatusReselect : (ok ? 0 : 1);
+    }
+}
+
+// final_rescore_wide_mw with eight float4 loads per thread in flight (8
+// pieces for up to 64 candidates, 4 for 128, 3 for 192, 2 for 256; deeper
+// windows spill).
+__device__ __forceinline__ void final_rescore_wide(const float* __restrict__ qp, float qn,
+                                                   const float* __restrict__ rows,
+                                                   const float* __restrict__ norms, int64_t n,
+                                                   int dim, int metric, uint32_t q,
+                                                   const uint64_t* top, int ncand, int kc,
+                                                   uint64_t* res, float* stage, const FlatArgs& fa,
+                                                   int proof, uint64_t sel_cut) {
+    if (ncand <= 64)
+        final_rescore_wide_mw<1, 8>(qp, qn, rows, norms, n, dim, metric, q, top, ncand, kc, res, stage, fa, proof, sel_cut);
+    else if (ncand <= 128)
+        final_rescore_wide_mw<2, 4>(qp, qn, rows, norms, n, dim, metric, q, top, ncand, kc, res, stage, fa, proof, sel_cut);
+    else if (ncand <= 192)
+        final_rescore_wide_mw<3, 3>(qp, qn, rows, norms, n, dim, metric, q, top, ncand, kc, res, stage, fa, proof, sel_cut);
+    else
+        final_rescore_wide_mw<4, 2>(qp, qn, rows, norms, n, dim, metric, q, top, ncand, kc, res, stage, fa, proof, sel_cut);
+}
+
 }  // namespace mans
