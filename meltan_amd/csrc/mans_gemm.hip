@@ -620,14 +620,13 @@ __global__ __launch_bounds__(512, 1) void flat_gemm_bf16x3(
 
 // grid (1, nq): bound[q] = the kc-th smallest slot of the query's sampled
 // lists (kEmptySlot when they hold fewer than kc).
-__global__ __launch_bounds__(256) void lists_kth_slot(int kc, int cap, int64_t per_query,
+__global__ __launch_bounds__(256) void lists_kth_slot(int kc, int64_t per_query,
                                                       const uint64_t* __restrict__ lists,
                                                       uint64_t* __restrict__ bound) {
     extern __shared__ uint64_t lds[];
     const uint32_t q = blockIdx.y;
-    WaveTopK sel;
-    block_select_lists(lists + (size_t)q * per_query, per_query, lds, cap, kc, sel);
-    if (threadIdx.x == 0) bound[q] = lds[kc - 1];
+    const uint64_t kth = block_kth_slot(lists + (size_t)q * per_query, per_query, kc, lds);
+    if (threadIdx.x == 0) bound[q] = kth;
 }
 
 // grid (1, nq): one block per query selects the kc smallest keys over its
@@ -809,7 +808,8 @@ hipError_t launch_bf3_bounds(const GemmPlan& p, int64_t nq, const uint64_t* list
                              hipStream_t s) {
     const int64_t per_query = (int64_t)p.s_nseg * kBf3Lists * gemm_list_len(p.kc);
     hipLaunchKernelGGL(lists_kth_slot, dim3(1, (unsigned)nq), dim3(256),
-                       sizeof(uint64_t) * 4 * (size_t)p.cap, s, p.kc, p.cap, per_query, lists, bound);
+                       per_query <= kKthLdsSlots ? sizeof(uint64_t) * (size_t)per_query : 0, s, p.kc,
+                       per_query, lists, bound);
     return hipGetLastError();
 }
 

@@ -917,15 +917,14 @@ __global__ __launch_bounds__(256) void int8_lists_merge(
 
 // grid (1, nq): each query's bound, the kc-th smallest slot of its lists
 // from the sampled launch (kEmptySlot when they hold fewer than kc).
-__global__ __launch_bounds__(256) void int8_lists_bound(int kc, int cap, int nlists,
+__global__ __launch_bounds__(256) void int8_lists_bound(int kc, int nlists,
                                                         const uint64_t* __restrict__ lists,
                                                         uint64_t* __restrict__ qbound) {
     extern __shared__ uint64_t lds[];
     const uint32_t q = blockIdx.y;
-    WaveTopK sel;
-    block_select_lists(lists + (size_t)q * nlists * kI8List, (int64_t)nlists * kI8List, lds, cap,
-                       kc, sel);  // ends in a barrier
-    if (threadIdx.x == 0) qbound[q] = lds[kc - 1];
+    const uint64_t kth = block_kth_slot(lists + (size_t)q * nlists * kI8List,
+                                        (int64_t)nlists * kI8List, kc, lds);
+    if (threadIdx.x == 0) qbound[q] = kth;
 }
 
 static bool i8gemm_ks(int stride, int* ks) {
@@ -1409,10 +1408,10 @@ static int int8_search_run(mans_ctx* ctx, mans_corpus* c, const float* d_q, int6
         ctx->time_begin(slot, st);
         e = launch_i8gemm(gp, pl, n, qcodes, coefs, nq, (int)metric, true, nullptr, lists, st);
         if (e == hipSuccess) {
-            const int bcap = flat_cap_for((int)kc);
+            const int64_t slots = (int64_t)2 * gp.s_nseg * kI8List;
             hipLaunchKernelGGL(int8_lists_bound, dim3(1, (unsigned)nq), dim3(256),
-                               sizeof(uint64_t) * 4 * (size_t)bcap, st, (int)kc, bcap, 2 * gp.s_nseg,
-                               (const uint64_t*)lists, qbound);
+                               slots <= kKthLdsSlots ? sizeof(uint64_t) * (size_t)slots : 0, st,
+                               (int)kc, 2 * gp.s_nseg, (const uint64_t*)lists, qbound);
             e = hipGetLastError();
         }
         ctx->time_end(slot, st, "int8_bound");

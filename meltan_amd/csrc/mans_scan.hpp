@@ -901,4 +901,21 @@ __device__ __forceinline__ void final_rescore_wide(const float* __restrict__ qp,
         final_rescore_wide_mw<4, 2>(qp, qn, rows, norms, n, dim, metric, q, top, ncand, kc, res, stage, fa, proof, sel_cut);
 }
 
+// The kc-th smallest of `total` slots at src (written by an earlier launch;
+// empty slots, kEmptySlot, are the largest values): kEmptySlot when fewer
+// than kc are not empty.  Up to kKthLdsSlots slots are read once into
+// lds; more are read from memory on every radix pass.
+constexpr int kKthLdsSlots = 4096;
+__device__ __forceinline__ uint64_t block_kth_slot(const uint64_t* __restrict__ src, int64_t total,
+                                                   int kc, uint64_t* lds) {
+    __shared__ uint32_t hist[256];
+    const bool in_lds = total <= kKthLdsSlots;
+    if (in_lds)
+        for (int64_t i = threadIdx.x; i < total; i += blockDim.x) lds[i] = src[i];
+    __syncthreads();
+    uint64_t kth;
+    block_radix_cut([&](int64_t i) { return in_lds ? lds[i] : src[i]; }, total, kc, hist, &kth);
+    return kth;
+}
+
 }  // namespace mans
