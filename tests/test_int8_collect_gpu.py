@@ -105,3 +105,38 @@ def test_int8_collect_small_batch_and_zero_query(gpu_ctx):
         ref = _oracle_rows(corpus, norms, planes, queries, 10, metric, mode=mode, budget=budget)
         _assert_same(gd, gi, ref, 10, f"batch m{metric} mode{mode}")
     c.release()
+
+
+def test_int8_collect_adversarial_rounds(gpu_ctx):
+    # The zero / duplicate / extreme-magnitude layout of
+    # BoundedExactScanTests.swift:211-250 at a size that takes the collect
+    # path: proofs that fail in the first round re-run on the list-based
+    # scan with the codes the sampled launch stored, and every round count
+    # and result must still equal the oracle's.
+    dim, n = 64, 140000
+    rows = workloads.lcg_vectors(1, n, dim, seed=3024)
+    corpus = rows.copy()
+    corpus[0::4] = 0.0
+    corpus[1::4] = rows[0]
+    idx = np.arange(n)
+    corpus[idx % 8 == 2] *= 1e-5
+    corpus[idx % 8 == 6] *= 1e5
+    norms = oracle.row_norms(corpus)
+    planes = oracle.int8_build(corpus)
+    c = gpu_ctx.upload(corpus)
+    q = workloads.lcg_vectors(1, 3, dim, seed=3025)
+    for metric in (COS, L2, IP):
+        for k in (10, 16):  # mode 0 starts at kc = max(256, 16 k)
+            print(f"int8 collect adversarial m{metric} k{k}", flush=True)
+            gd, gi, rounds, launches = _run(gpu_ctx, c, q, k, metric, 0, 0)
+            assert launches["int8_bound"] == 1, launches
+            ref = _oracle_rows(corpus, norms, planes, q, k, metric)
+            _assert_same(gd, gi, ref, k, f"collect adversarial m{metric} k{k}")
+            # Rounds past a budget of 1024 end in the exact scan, so the
+            # round counts are compared where the oracle stops by then.
+            finals = [oracle.int8_search(corpus, norms, planes, qq, k, metric)[2] for qq in q]
+            for r, f in zip(rounds, finals):
+                if f <= 1024:
+                    assert r == _rounds_for(f, k, n)
+            check_flat(corpus, norms, q, k, metric, gd, gi, f"collect adversarial exact m{metric} k{k}")
+    c.release()
