@@ -638,8 +638,7 @@ __global__ __launch_bounds__(256) void flat_lists_merge(
     const uint64_t* __restrict__ lists, const uint64_t* __restrict__ qbound,
     const uint32_t* __restrict__ qbad, FlatArgs fa) {
     extern __shared__ uint64_t lds[];
-    __shared__ uint32_t cut_bits;
-    const int lr = threadIdx.x & 15;
+    const int tid = threadIdx.x, lr = tid & 15;
     const uint32_t q = blockIdx.y;
     const int dim4 = dim >> 2;
     const float* qp = queries + (int64_t)q * dim;
@@ -649,25 +648,57 @@ __global__ __launch_bounds__(256) void flat_lists_merge(
         const int idx = lr + 16 * c;
         qv[c] = idx < dim4 ? *reinterpret_cast<const f4v*>(qp + 4 * idx) : f4v{0.f, 0.f, 0.f, 0.f};
     }
+    // q.q in the dots.c order (every lane of a 16-lane group gets it).
+    const float qn = metric == kMetricIP ? 0.0f : chain_dot<NCH>(qv, qv, dim4);
     const uint64_t* lq = lists + (size_t)q * nlists * list_len;
-    if (threadIdx.x == 0) cut_bits = 0xFFFFFFFFu;
-    __syncthreads();
-    // Smallest largest key over the full lists (ordered key bits).
-    uint32_t mine = 0xFFFFFFFFu;
-    for (int i = threadIdx.x; i < nlists; i += blockDim.x) {
+    const int64_t total = (int64_t)nlists * list_len;
+    uint64_t* top = lds;         // 256 slots
+    uint64_t* res = lds + 256;   // 256 slots
+    uint64_t* cand = lds + 512;  // the lists' slots, then the rescore stage
+    // Smallest largest slot over the full lists: its key bounds the rows
+    // the lists turned away.
+    uint64_t mine = kEmptySlot;
+    for (int i = tid; i < nlists; i += blockDim.x) {
         const uint64_t last = lq[(size_t)i * list_len + list_len - 1];
-        if (last != kEmptySlot) mine = min(mine, (uint32_t)(last >> 32));
+        mine = last < mine ? last : mine;
     }
-    atomicMin(&cut_bits, mine);
-    WaveTopK sel;
-    block_select_lists(lq, (int64_t)nlists * list_len, lds, cap, kc, sel);  // ends in a barrier
-    float list_cut = cut_bits == 0xFFFFFFFFu ? kFltMax : from_ordered_bits(cut_bits);
+    const uint64_t full_cut = block_reduce_u64<false>(mine);
+    const bool in_lds = total <= kKthLdsSlots;
+    if (in_lds)
+        for (int64_t i = tid; i < total; i += blockDim.x) cand[i] = lq[i];
+    __shared__ uint32_t hist[256];
+    __shared__ int ntop;
+    if (tid == 0) ntop = 0;
+    __syncthreads();
+    // The kc smallest slots (empty slots are the largest values and are
+    // never taken).
+    auto get = [&](int64_t i) { return in_lds ? cand[i] : lq[i]; };
+    uint64_t kth;
+    const uint64_t sel = block_radix_cut(get, total, kc, hist, &kth);
+    for (int64_t i = tid; i < total; i += blockDim.x) {
+        const uint64_t s = get(i);
+        if (s != kEmptySlot && s <= sel) {
+            const int p = atomicAdd(&ntop, 1);
+            if (p < 256) top[p] = s;
+        }
+    }
+    __syncthreads();
+    const int ncand = ntop < kc ? ntop : kc;
+    prefetch_rows(rows, top, ncand, dim, res);
+    int sort_n = 64;
+    while (sort_n < kc) sort_n <<= 1;
+    for (int i = ncand + tid; i < sort_n; i += blockDim.x) top[i] = kEmptySlot;
+    __syncthreads();
+    if (tid < 64) wave_bitonic_sort(top, sort_n);
+    __syncthreads();
+    float list_cut = full_cut == kEmptySlot ? kFltMax : slot_key(full_cut);
     // Rows above the query's bound were never admitted: their keys are >= it.
     if (qbound && qbound[q] != kEmptySlot) list_cut = fminf(list_cut, slot_key(qbound[q]));
-    final_rescore_f4<NCH>(qv, rows, norms, n, dim, metric, q, lds, kc, fa, list_cut);
+    final_rescore_wide(qp, qn, rows, norms, n, dim, metric, q, top, ncand, kc, res,
+                       reinterpret_cast<float*>(cand), fa, kProofFlat, kEmptySlot, list_cut);
     // A query with values outside the split range has no valid keys here:
     // the streaming scan runs it again.
-    if (threadIdx.x == 0 && qbad && qbad[q]) fa.status[q] = 1;
+    if (tid == 0 && qbad && qbad[q]) fa.status[q] = 1;
 }
 
 // ---------------------------------------------------------------------------
@@ -852,7 +883,11 @@ static void launch_lists_merge(const GemmPlan& p, const float* rows, const float
                                int dim, const float* queries, int64_t nq, int metric,
                                const uint64_t* lists, const uint64_t* qbound,
                                const uint32_t* qbad, const FlatArgs& fa, hipStream_t s) {
-    size_t shmem = sizeof(uint64_t) * 4 * (size_t)p.cap;
+    const int64_t total = (int64_t)p.lps * p.nseg * gemm_list_len(p.kc);
+    static_assert(kGemmMaxKc <= 64, "the merge's rescore stages one group of 64 rows");
+    const size_t stage = sizeof(float) * 2 * 64 * kWideStride;
+    const size_t slots = total <= kKthLdsSlots ? sizeof(uint64_t) * (size_t)total : 0;
+    const size_t shmem = sizeof(uint64_t) * 512 + std::max(stage, slots);
     hipLaunchKernelGGL(flat_lists_merge<NCH>, dim3(1, (unsigned)nq), dim3(256), shmem, s, rows,
                        norms, n, dim, queries, metric, p.kc, p.cap, p.lps * p.nseg,
                        gemm_list_len(p.kc), lists, qbound, qbad, fa);

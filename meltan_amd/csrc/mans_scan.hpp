@@ -770,8 +770,8 @@ __device__ __forceinline__ void prefetch_rows(const float* __restrict__ rows, co
 // float4 loads per thread and piece) and written one piece ahead of the
 // threads that read them.  qp: the query (read with scalar loads); qn: its
 // sequential q.q.  res: 256 slots (it may be the sink of prefetch_rows);
-// stage: 2 * 64 M * kWideStride floats.  Outputs, proof and sel_cut as
-// final_rescore_f4 (status at blockIdx.y).  dim % 4 == 0.
+// stage: 2 * 64 M * kWideStride floats.  Outputs, proof, list_cut and
+// sel_cut as final_rescore_f4 (status at blockIdx.y).  dim % 4 == 0.
 constexpr int kWidePiece = 16;
 constexpr int kWideStride = 20;  // floats per staged row piece (bank spread)
 template <int M, int W>
@@ -781,7 +781,7 @@ __device__ __forceinline__ void final_rescore_wide_mw(const float* __restrict__ 
                                                       int dim, int metric, uint32_t q,
                                                       const uint64_t* top, int ncand, int kc,
                                                       uint64_t* res, float* stage, const FlatArgs& fa,
-                                                      int proof, uint64_t sel_cut) {
+                                                      int proof, uint64_t sel_cut, float list_cut) {
     const int tid = threadIdx.x;
     const int npieces = (dim + kWidePiece - 1) / kWidePiece;
     const int lr = tid >> 2, u = tid & 3;  // stages float4 u of rows lr + 64 m
@@ -863,7 +863,9 @@ __device__ __forceinline__ void final_rescore_wide_mw(const float* __restrict__ 
         fa.out_ids[(int64_t)q * fa.k_stride + i] = id;
     }
     if (tid == 0) {
-        const float cutoff = ncand > 0 ? slot_key(top[ncand - 1]) : 0.0f;
+        // list_cut: rows that bounded lists turned away have keys >= it.
+        float cutoff = ncand > 0 ? slot_key(top[ncand - 1]) : 0.0f;
+        cutoff = cutoff < list_cut ? cutoff : list_cut;
         const bool all_rows = (int64_t)ncand >= n;
         bool ok;
         if (proof == kProofNone) {
@@ -890,15 +892,16 @@ __device__ __forceinline__ void final_rescore_wide(const float* __restrict__ qp,
                                                    int dim, int metric, uint32_t q,
                                                    const uint64_t* top, int ncand, int kc,
                                                    uint64_t* res, float* stage, const FlatArgs& fa,
-                                                   int proof, uint64_t sel_cut) {
+                                                   int proof, uint64_t sel_cut,
+                                                   float list_cut = kFltMax) {
     if (ncand <= 64)
-        final_rescore_wide_mw<1, 8>(qp, qn, rows, norms, n, dim, metric, q, top, ncand, kc, res, stage, fa, proof, sel_cut);
+        final_rescore_wide_mw<1, 8>(qp, qn, rows, norms, n, dim, metric, q, top, ncand, kc, res, stage, fa, proof, sel_cut, list_cut);
     else if (ncand <= 128)
-        final_rescore_wide_mw<2, 4>(qp, qn, rows, norms, n, dim, metric, q, top, ncand, kc, res, stage, fa, proof, sel_cut);
+        final_rescore_wide_mw<2, 4>(qp, qn, rows, norms, n, dim, metric, q, top, ncand, kc, res, stage, fa, proof, sel_cut, list_cut);
     else if (ncand <= 192)
-        final_rescore_wide_mw<3, 3>(qp, qn, rows, norms, n, dim, metric, q, top, ncand, kc, res, stage, fa, proof, sel_cut);
+        final_rescore_wide_mw<3, 3>(qp, qn, rows, norms, n, dim, metric, q, top, ncand, kc, res, stage, fa, proof, sel_cut, list_cut);
     else
-        final_rescore_wide_mw<4, 2>(qp, qn, rows, norms, n, dim, metric, q, top, ncand, kc, res, stage, fa, proof, sel_cut);
+        final_rescore_wide_mw<4, 2>(qp, qn, rows, norms, n, dim, metric, q, top, ncand, kc, res, stage, fa, proof, sel_cut, list_cut);
 }
 
 // The kc-th smallest of `total` slots at src (written by an earlier launch;
