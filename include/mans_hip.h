@@ -98,9 +98,10 @@ int mans_corpus_upload_f32(mans_ctx *ctx, const float *rows, int64_t n, int64_t 
  *
  * mans_mann_inspect validates a file as MmapIndexLoader.load does (magic,
  * version, metric and storage codes, non-zero counts, section and trailer
- * bounds, entry point below the node count; the IDMap JSON itself is not
- * decoded) and fills `info`; MANS_CORRUPT_FILE with the reference's reason
- * otherwise.  Needs no device. */
+ * bounds, an IDMap JSON payload that decodes with exactly node-count entries
+ * (MmapIndexLoader.swift:174-182), entry point below the node count) and
+ * fills `info`; MANS_CORRUPT_FILE with the reference's reason otherwise.
+ * Needs no device. */
 typedef struct mans_mann_info {
     uint32_t version, node_count, degree, dim, metric, storage_type, entry_point;
     int64_t page_size;
@@ -163,12 +164,23 @@ int mans_int8_codes_download(mans_ctx *ctx, mans_corpus *corpus, int8_t *codes, 
  * order and rows packed list by list (IVFFlatSearch.swift:589-615). */
 int mans_ivf_flat_build(mans_ctx *ctx, const mans_corpus *corpus, const float *centroids,
                         int64_t nlist, uint32_t metric, mans_ivf **out);
-/* Lloyd k-means on the device (strided-sample initialisation, fp64 means in
- * row order); produces centroids for mans_ivf_flat_build.  The reference
- * trains with KMeans.cluster (KMeans.swift:53-257), whose Swift RNG cannot
- * be reproduced; this routine is deterministic. */
+/* Lloyd k-means on the device, KMeans.cluster (KMeans.swift:53-257):
+ * assignment by SIMDDistance.distance (SIMDDistance.swift:17-80) with strict
+ * < (the first centroid wins ties); the loop stops when no assignment
+ * changes; each centroid is its rows' float sum in row order times
+ * 1/count (the single-worker order, KMeans.swift:208-250); empty clusters
+ * keep their centroid.  The reference seeds k-means++ from Swift's stdlib
+ * RNG, which is not reproduced: the initial centroids are rows 0, s, 2s, ...
+ * with s = max(1, n / k). */
 int mans_kmeans(mans_ctx *ctx, const mans_corpus *corpus, int64_t k, int64_t iters,
                 uint32_t metric, float *out_centroids);
+/* The centroids IVFFlatSearch.buildPartition trains
+ * (IVFFlatSearch.swift:517-551): L = min(max(1, nlist), n) lists, a strided
+ * sample of min(n, max(L, min(4096, 16 L))) rows, mans_kmeans on the sample
+ * with 8 iterations and the index's metric.  Writes L x dim centroids
+ * (out_centroids holds nlist x dim floats) and L to out_nlist. */
+int mans_ivf_flat_train(mans_ctx *ctx, const mans_corpus *corpus, int64_t nlist, uint32_t metric,
+                        float *out_centroids, int64_t *out_nlist);
 /* IVFFlatSearch.search over a built partition (IVFFlatSearch.swift:115-137,
  * 214-291).  out_probes (nullable): nq x nprobe list ids, ascending. */
 int mans_ivf_flat_search(mans_ctx *ctx, const mans_ivf *ivf, const float *queries, int64_t nq,
@@ -181,6 +193,15 @@ int mans_ivf_flat_search_device(mans_ctx *ctx, const mans_ivf *ivf, const float 
 int mans_ivf_download_lists(const mans_ivf *ivf, int64_t *offsets, uint32_t *list_ids);
 void mans_ivf_release(mans_ivf *ivf);
 
+/* _IVFPQIndex.train (IVFPQIndex.swift:54-104) on the rows of `train`:
+ * coarse k-means (nlist, iters, metric; mans_kmeans), each row's residual
+ * against its centroid from the last assignment, then
+ * ProductQuantizer.train (ProductQuantizer.swift:10-85): per subspace
+ * k-means of the residual subvectors with 256 centroids, L2 and iters
+ * iterations, same rules.  Needs n >= 256, n >= nlist and dim % m == 0.
+ * out_coarse: nlist x dim; out_codebooks: m x 256 x dim/m. */
+int mans_ivfpq_train(mans_ctx *ctx, const mans_corpus *train, int64_t nlist, int64_t m,
+                     int64_t iters, uint32_t metric, float *out_coarse, float *out_codebooks);
 /* IVF-PQ: coarse centroids (nlist x dim) and codebooks (M x 256 x dim/M)
  * are given (trained by the caller, IVFPQIndex.swift:54-104).  Adds every
  * corpus row: coarse assignment (IVFPQIndex.swift:514-550) and
@@ -203,6 +224,16 @@ int mans_ivfpq_search_device(mans_ctx *ctx, const mans_ivfpq *pq, const float *d
                              float *d_out_score, uint32_t *d_out_ids, void *stream);
 /* Copies codes back in row order (n x M) plus coarse assignments (n). */
 int mans_ivfpq_download_codes(const mans_ivfpq *pq, uint8_t *codes, int32_t *assign);
+/* Binary persistence of a built index, in place of the JSON "IVFP" state of
+ * _IVFPQIndex.save/load (IVFPQIndex.swift:252-324), which does not scale to
+ * 10M codes: a 48-byte header ("IVPB", version 1, dim, metric, n, nlist, m,
+ * dim/m), then the coarse centroids, codebooks, list offsets, list ids,
+ * codes (list by list) and coarse assignments, little-endian.  Load
+ * validates the file
+ * (MANS_CORRUPT_FILE with a reason) and uploads it; `corpus` (nullable)
+ * serves the exact rerank and must hold the same n x dim rows. */
+int mans_ivfpq_save(const mans_ivfpq *pq, const char *path);
+int mans_ivfpq_load(mans_ctx *ctx, const mans_corpus *corpus, const char *path, mans_ivfpq **out);
 void mans_ivfpq_release(mans_ivfpq *pq);
 
 /* Kernel timing with HIP events on the stream each kernel runs on.

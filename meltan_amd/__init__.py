@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
+import struct
 from pathlib import Path
 
 import numpy as np
@@ -51,9 +52,11 @@ EXPORTS = [
     "mans_mann_inspect", "mans_corpus_upload_mann", "mans_corpus_write_rows", "mans_corpus_invalidate", "mans_corpus_release",
     "mans_corpus_count", "mans_corpus_dim", "mans_flat_search", "mans_flat_search_device",
     "mans_int8_search", "mans_int8_search_device", "mans_int8_codes_download",
-    "mans_ivf_flat_build", "mans_kmeans", "mans_ivf_flat_search", "mans_ivf_flat_search_device",
-    "mans_ivf_download_lists", "mans_ivf_release", "mans_ivfpq_build", "mans_ivfpq_search",
-    "mans_ivfpq_search_device", "mans_ivfpq_download_codes", "mans_ivfpq_release",
+    "mans_ivf_flat_build", "mans_kmeans", "mans_ivf_flat_train", "mans_ivf_flat_search",
+    "mans_ivf_flat_search_device", "mans_ivf_download_lists", "mans_ivf_release",
+    "mans_ivfpq_train", "mans_ivfpq_build", "mans_ivfpq_search",
+    "mans_ivfpq_search_device", "mans_ivfpq_download_codes", "mans_ivfpq_save", "mans_ivfpq_load",
+    "mans_ivfpq_release",
     "mans_timing_enable", "mans_timing_read", "mans_timing_reset",
 ]
 
@@ -123,6 +126,10 @@ def lib() -> C.CDLL:
         L.mans_int8_codes_download.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp]
         L.mans_ivf_flat_build.argtypes = [_vp, _vp, _vp, _i64, _u32, C.POINTER(_vp)]
         L.mans_kmeans.argtypes = [_vp, _vp, _i64, _i64, _u32, _vp]
+        L.mans_ivf_flat_train.argtypes = [_vp, _vp, _i64, _u32, _vp, C.POINTER(_i64)]
+        L.mans_ivfpq_train.argtypes = [_vp, _vp, _i64, _i64, _i64, _u32, _vp, _vp]
+        L.mans_ivfpq_save.argtypes = [_vp, C.c_char_p]
+        L.mans_ivfpq_load.argtypes = [_vp, _vp, C.c_char_p, C.POINTER(_vp)]
         L.mans_ivf_flat_search.argtypes = [_vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp]
         L.mans_ivf_flat_search_device.argtypes = [_vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp]
         L.mans_ivf_download_lists.argtypes = [_vp, _vp, _vp]
@@ -305,6 +312,24 @@ class Corpus:
                                  _ptr(out)))
         return out
 
+    def ivf_flat_train(self, nlist: int, metric="l2") -> np.ndarray:
+        """IVFFlatSearch.buildPartition's sampled 8-iteration k-means:
+        min(nlist, n) x dim centroids."""
+        out = np.empty((max(1, nlist), self.dim), dtype=np.float32)
+        lists = _i64()
+        _check(lib().mans_ivf_flat_train(self.ctx.handle, self.handle, nlist, metric_code(metric),
+                                         _ptr(out), C.byref(lists)))
+        return out[:lists.value]
+
+    def ivfpq_train(self, nlist: int, m: int, iters: int, metric="innerProduct"):
+        """_IVFPQIndex.train on these rows: (coarse nlist x dim, codebooks
+        m x 256 x dim/m)."""
+        coarse = np.empty((nlist, self.dim), dtype=np.float32)
+        books = np.empty((m, 256, self.dim // m), dtype=np.float32)
+        _check(lib().mans_ivfpq_train(self.ctx.handle, self.handle, nlist, m, iters,
+                                      metric_code(metric), _ptr(coarse), _ptr(books)))
+        return coarse, books
+
     def ivf_flat_build(self, centroids, metric="l2") -> "IVFFlat":
         c = _f32(centroids, self.dim)
         h = _vp()
@@ -319,7 +344,7 @@ class Corpus:
         h = _vp()
         _check(lib().mans_ivfpq_build(self.ctx.handle, self.handle, _ptr(c), c.shape[0], _ptr(cb),
                                       m, metric_code(metric), C.byref(h)))
-        return IVFPQ(self, h, c.shape[0], m)
+        return IVFPQ(self.ctx, self, h, c.shape[0], m, self.n, self.dim)
 
 
 class IVFFlat:
@@ -362,11 +387,15 @@ class IVFFlat:
 
 
 class IVFPQ:
-    def __init__(self, corpus: Corpus, handle, nlist: int, m: int):
-        self.corpus = corpus
+    def __init__(self, ctx: Context, corpus: "Corpus | None", handle, nlist: int, m: int, n: int,
+                 dim: int):
+        self.ctx = ctx
+        self.corpus = corpus  # rows of the exact rerank (None after a load without them)
         self.handle = handle
         self.nlist = nlist
         self.m = m
+        self.n = n
+        self.dim = dim
 
     def release(self) -> None:
         if self.handle:
@@ -380,23 +409,40 @@ class IVFPQ:
             pass
 
     def search(self, queries, k_adc: int, nprobe: int, rerank_k: int = 0):
-        q = _f32(queries, self.corpus.dim)
+        q = _f32(queries, self.dim)
         nq = q.shape[0]
         kout = rerank_k if rerank_k > 0 else k_adc
         score = np.empty((nq, kout), dtype=np.float32)
         ids = np.empty((nq, kout), dtype=np.uint32)
-        _check(lib().mans_ivfpq_search(self.corpus.ctx.handle, self.handle, _ptr(q), nq, k_adc,
+        _check(lib().mans_ivfpq_search(self.ctx.handle, self.handle, _ptr(q), nq, k_adc,
                                        nprobe, rerank_k, _ptr(score), _ptr(ids)))
         return score, ids
 
     def search_device(self, d_queries: int, nq: int, k_adc: int, nprobe: int, rerank_k: int,
                       d_score: int, d_ids: int, stream: int | None = None) -> None:
-        _check(lib().mans_ivfpq_search_device(self.corpus.ctx.handle, self.handle, d_queries, nq,
+        _check(lib().mans_ivfpq_search_device(self.ctx.handle, self.handle, d_queries, nq,
                                               k_adc, nprobe, rerank_k, d_score, d_ids, stream))
 
     def codes(self):
-        n = self.corpus.n
-        codes = np.empty((n, self.m), dtype=np.uint8)
-        assign = np.empty(n, dtype=np.int32)
+        codes = np.empty((self.n, self.m), dtype=np.uint8)
+        assign = np.empty(self.n, dtype=np.int32)
         _check(lib().mans_ivfpq_download_codes(self.handle, _ptr(codes), _ptr(assign)))
         return codes, assign
+
+    def save(self, path) -> None:
+        """Binary persistence (mans_ivfpq_save)."""
+        _check(lib().mans_ivfpq_save(self.handle, str(path).encode()))
+
+
+IVPB_HEADER = struct.Struct("<4s3I2Q2IQ")  # magic, version, dim, metric, n, nlist, m, dsub, reserved
+
+
+def ivfpq_load(ctx: Context, path, corpus: "Corpus | None" = None) -> IVFPQ:
+    """mans_ivfpq_load: a saved index onto the device; `corpus` serves the
+    exact rerank."""
+    h = _vp()
+    _check(lib().mans_ivfpq_load(ctx.handle, corpus.handle if corpus else None,
+                                 str(path).encode(), C.byref(h)))
+    with open(path, "rb") as f:
+        _, _, dim, _, n, nlist, m, _, _ = IVPB_HEADER.unpack(f.read(IVPB_HEADER.size))
+    return IVFPQ(ctx, corpus, h, nlist, m, n, dim)

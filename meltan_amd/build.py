@@ -53,14 +53,24 @@ def build_datagen() -> Path:
     return out
 
 
-def build_hip(jobs: int | None = None) -> Path:
+def _stale(src: Path, obj: Path) -> bool:
+    """True when obj is missing or older than src or any shared header."""
+    if not obj.exists():
+        return True
+    t = obj.stat().st_mtime
+    deps = [src, *CSRC.glob("*.hpp"), ROOT / "include" / "mans_hip.h"]
+    return any(d.stat().st_mtime > t for d in deps)
+
+
+def build_hip(jobs: int | None = None, incremental: bool = False) -> Path:
+    """Compiles every .hip source (only the stale ones when incremental)."""
     OBJ.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     objects = [OBJ / (s.stem + ".o") for s in sources]
-    jobs = jobs or min(len(sources), max(1, (os.cpu_count() or 4)))
+    todo = [(s, o) for s, o in zip(sources, objects) if not incremental or _stale(s, o)]
+    jobs = jobs or min(max(1, len(todo)), max(1, (os.cpu_count() or 4)))
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        futs = [ex.submit(_run, [HIPCC, *HIP_FLAGS, "-c", str(s), "-o", str(o)])
-                for s, o in zip(sources, objects)]
+        futs = [ex.submit(_run, [HIPCC, *HIP_FLAGS, "-c", str(s), "-o", str(o)]) for s, o in todo]
         for f in futs:
             f.result()
     out = PKG / "libmans_hip.so"
@@ -71,11 +81,11 @@ def build_hip(jobs: int | None = None) -> Path:
     return out
 
 
-def build_all() -> None:
+def build_all(incremental: bool = False) -> None:
     build_datagen()
-    build_hip()
+    build_hip(incremental=incremental)
 
 
 if __name__ == "__main__":
-    build_all()
+    build_all(incremental="--incremental" in sys.argv)
     print("built", PKG / "libmans_hip.so", PKG / "libmans_datagen.so")

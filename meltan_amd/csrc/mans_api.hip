@@ -237,6 +237,214 @@ static bool align_up(int64_t v, int64_t a, int64_t* out) {
     return r == 0 ? (*out = v, true) : add_ok(v, a - r, out);
 }
 
+// The IDMap payload as JSONDecoder decodes IDMap (IDMap.swift:88-111): a
+// top-level object with externalToInternal ([String: UInt32], a JSON object),
+// internalToExternal ([UInt32: String]) and nextID (UInt32) required, and
+// numericToInternal ([UInt64: UInt32]) / internalToNumeric optional.
+// Dictionaries whose keys are integers are encoded as flat arrays of
+// alternating keys and values; an object with decimal keys is accepted too.
+// Unknown keys are ignored.  The count is IDMap.count: the distinct keys of
+// externalToInternal plus those of numericToInternal.
+namespace {
+
+struct JsonReader {
+    const char* p;
+    const char* e;
+    void ws() {
+        while (p < e && (*p == ' ' || *p == '\n' || *p == '\r' || *p == '\t')) ++p;
+    }
+    bool eat(char c) {
+        ws();
+        if (p < e && *p == c) {
+            ++p;
+            return true;
+        }
+        return false;
+    }
+    bool peek(char c) {
+        ws();
+        return p < e && *p == c;
+    }
+    // A string (escapes decoded for \uXXXX below 0x80 and the one-letter
+    // escapes; other code points are kept as their escape text).
+    bool string(std::string* out) {
+        ws();
+        if (p >= e || *p != '"') return false;
+        ++p;
+        if (out) out->clear();
+        while (p < e && *p != '"') {
+            char c = *p++;
+            if ((unsigned char)c < 0x20) return false;
+            if (c == '\\') {
+                if (p >= e) return false;
+                const char x = *p++;
+                switch (x) {
+                case '"': case '\\': case '/': break;
+                case 'b': c = '\b'; break;
+                case 'f': c = '\f'; break;
+                case 'n': c = '\n'; break;
+                case 'r': c = '\r'; break;
+                case 't': c = '\t'; break;
+                case 'u': {
+                    if (e - p < 4) return false;
+                    unsigned v = 0;
+                    for (int i = 0; i < 4; ++i) {
+                        const char h = p[i];
+                        v <<= 4;
+                        if (h >= '0' && h <= '9') v |= (unsigned)(h - '0');
+                        else if (h >= 'a' && h <= 'f') v |= (unsigned)(h - 'a' + 10);
+                        else if (h >= 'A' && h <= 'F') v |= (unsigned)(h - 'A' + 10);
+                        else return false;
+                    }
+                    if (out) {
+                        if (v < 0x80) out->push_back((char)v);
+                        else out->append(p - 2, 6);
+                    }
+                    p += 4;
+                    continue;
+                }
+                default: return false;
+                }
+                c = x == '"' || x == '\\' || x == '/' ? x : c;
+            }
+            if (out) out->push_back(c);
+        }
+        if (p >= e) return false;
+        ++p;
+        return true;
+    }
+    // A non-negative integer literal no larger than `max`.
+    bool uint(uint64_t max, uint64_t* v) {
+        ws();
+        const char* s = p;
+        uint64_t x = 0;
+        while (p < e && *p >= '0' && *p <= '9') {
+            const uint64_t d = (uint64_t)(*p - '0');
+            if (x > (max - d) / 10) return false;
+            x = x * 10 + d;
+            ++p;
+        }
+        if (p == s || (p - s > 1 && *s == '0')) return false;
+        if (p < e && (*p == '.' || *p == 'e' || *p == 'E')) return false;
+        if (v) *v = x;
+        return true;
+    }
+    bool literal(const char* w) {
+        ws();
+        const size_t n = std::strlen(w);
+        if ((size_t)(e - p) < n || std::memcmp(p, w, n) != 0) return false;
+        p += n;
+        return true;
+    }
+    bool value(int depth) {  // any JSON value, skipped
+        if (depth > 64) return false;
+        ws();
+        if (p >= e) return false;
+        if (*p == '"') return string(nullptr);
+        if (*p == '{') {
+            ++p;
+            if (eat('}')) return true;
+            do {
+                if (!string(nullptr) || !eat(':') || !value(depth + 1)) return false;
+            } while (eat(','));
+            return eat('}');
+        }
+        if (*p == '[') {
+            ++p;
+            if (eat(']')) return true;
+            do {
+                if (!value(depth + 1)) return false;
+            } while (eat(','));
+            return eat(']');
+        }
+        if (*p == 't') return literal("true");
+        if (*p == 'f') return literal("false");
+        if (*p == 'n') return literal("null");
+        if (*p == '-') ++p;
+        const char* s = p;
+        while (p < e && ((*p >= '0' && *p <= '9') || *p == '.' || *p == 'e' || *p == 'E' ||
+                         *p == '+' || *p == '-'))
+            ++p;
+        return p > s;
+    }
+    // A dictionary with integer keys (below kmax) and values of kind `val`
+    // ('u': integer below vmax, 's': string): the alternating array or an
+    // object with decimal keys.  keys (nullable) receives the keys.
+    bool int_dict(uint64_t kmax, char val, uint64_t vmax, std::vector<uint64_t>* keys) {
+        auto one_value = [&]() { return val == 's' ? string(nullptr) : uint(vmax, nullptr); };
+        if (eat('[')) {
+            if (eat(']')) return true;
+            do {
+                uint64_t k;
+                if (!uint(kmax, &k) || !eat(',') || !one_value()) return false;
+                if (keys) keys->push_back(k);
+            } while (eat(','));
+            return eat(']');
+        }
+        if (!eat('{')) return false;
+        if (eat('}')) return true;
+        std::string ks;
+        do {
+            if (!string(&ks) || !eat(':') || !one_value()) return false;
+            JsonReader kr{ks.data(), ks.data() + ks.size()};
+            uint64_t k;
+            if (!kr.uint(kmax, &k) || kr.p != kr.e) return false;
+            if (keys) keys->push_back(k);
+        } while (eat(','));
+        return eat('}');
+    }
+};
+
+bool idmap_count(const uint8_t* data, int64_t len, int64_t* count) {
+    JsonReader r{(const char*)data, (const char*)data + len};
+    if (!r.eat('{')) return false;
+    bool have_e2i = false, have_i2e = false, have_next = false;
+    std::vector<std::string> ext;
+    std::vector<uint64_t> numeric;
+    std::string key;
+    if (!r.eat('}')) {
+        do {
+            if (!r.string(&key) || !r.eat(':')) return false;
+            if (key == "externalToInternal") {
+                have_e2i = true;
+                ext.clear();
+                if (!r.eat('{')) return false;
+                if (!r.eat('}')) {
+                    std::string s;
+                    do {
+                        if (!r.string(&s) || !r.eat(':') || !r.uint(0xFFFFFFFFull, nullptr)) return false;
+                        ext.push_back(s);
+                    } while (r.eat(','));
+                    if (!r.eat('}')) return false;
+                }
+            } else if (key == "internalToExternal") {
+                have_i2e = true;
+                if (!r.int_dict(0xFFFFFFFFull, 's', 0, nullptr)) return false;
+            } else if (key == "nextID") {
+                have_next = true;
+                if (!r.uint(0xFFFFFFFFull, nullptr)) return false;
+            } else if (key == "numericToInternal") {
+                numeric.clear();
+                if (!r.literal("null") && !r.int_dict(~0ull, 'u', 0xFFFFFFFFull, &numeric)) return false;
+            } else if (key == "internalToNumeric") {
+                if (!r.literal("null") && !r.int_dict(0xFFFFFFFFull, 'u', ~0ull, nullptr)) return false;
+            } else if (!r.value(0)) {
+                return false;
+            }
+        } while (r.eat(','));
+        if (!r.eat('}')) return false;
+    }
+    r.ws();
+    if (r.p != r.e || !have_e2i || !have_i2e || !have_next) return false;
+    std::sort(ext.begin(), ext.end());
+    std::sort(numeric.begin(), numeric.end());
+    *count = (int64_t)(std::unique(ext.begin(), ext.end()) - ext.begin()) +
+             (int64_t)(std::unique(numeric.begin(), numeric.end()) - numeric.begin());
+    return true;
+}
+
+}  // namespace
+
 // Validates the mapped bytes [base, base + len) as a MANN v3 file.
 static int mann_parse(const uint8_t* base, int64_t len, int64_t page, mans_mann_info* info) {
     std::memset(info, 0, sizeof(*info));
@@ -283,6 +491,10 @@ static int mann_parse(const uint8_t* base, int64_t len, int64_t page, mans_mann_
     if (!add_ok(tend, idmap, &idend) || !add_ok(idend, 4, &epend) || epend > len)
         return fail(MANS_CORRUPT_FILE, "Truncated IDMap payload");
     info->entry_point = read_le32(base + idend);
+    int64_t idcount = 0;
+    if (!idmap_count(base + tend, idmap, &idcount))
+        return fail(MANS_CORRUPT_FILE, "IDMap payload is corrupt");
+    if (idcount != n) return fail(MANS_CORRUPT_FILE, "ID map size does not match node count");
     if ((int64_t)info->entry_point >= n) return fail(MANS_CORRUPT_FILE, "Entry point is out of bounds");
     info->vector_offset = voff;
     info->vector_bytes = vbytes;
@@ -720,6 +932,7 @@ int mans_flat_search_device(mans_ctx* ctx, const mans_corpus* c, const float* d_
                             int64_t nq, int64_t k, uint32_t metric, float* d_out_dist,
                             uint32_t* d_out_ids, void* stream) {
     if (!ctx || !c) return fail(MANS_SEARCH_FAILED, "NULL context or corpus");
+    if (check_k(k) != MANS_OK) return MANS_SEARCH_FAILED;
     if (nq > 0 && k > 0 && (!d_queries || !d_out_dist || !d_out_ids))
         return fail(MANS_SEARCH_FAILED, "NULL buffer");
     DeviceGuard dg(ctx->device);
@@ -733,6 +946,7 @@ int mans_flat_search_device(mans_ctx* ctx, const mans_corpus* c, const float* d_
 int mans_flat_search(mans_ctx* ctx, const mans_corpus* c, const float* queries, int64_t nq,
                      int64_t k, uint32_t metric, float* out_dist, uint32_t* out_ids) {
     if (!ctx || !c) return fail(MANS_SEARCH_FAILED, "NULL context or corpus");
+    if (check_k(k) != MANS_OK) return MANS_SEARCH_FAILED;
     if (nq <= 0 || k <= 0) return MANS_OK;
     if (!queries || !out_dist || !out_ids) return fail(MANS_SEARCH_FAILED, "NULL buffer");
     DeviceGuard dg(ctx->device);

@@ -1512,6 +1512,7 @@ int mans_int8_search_device(mans_ctx* ctx, mans_corpus* c, const float* d_querie
                             int64_t k, uint32_t metric, int32_t mode, int64_t budget,
                             float* d_out_dist, uint32_t* d_out_ids, void* stream) {
     if (!ctx || !c) return fail(MANS_SEARCH_FAILED, "NULL context or corpus");
+    if (check_k(k) != MANS_OK) return MANS_SEARCH_FAILED;
     if (nq > 0 && k > 0 && (!d_queries || !d_out_dist || !d_out_ids))
         return fail(MANS_SEARCH_FAILED, "NULL buffer");
     DeviceGuard dg(ctx->device);
@@ -1526,6 +1527,7 @@ int mans_int8_search(mans_ctx* ctx, mans_corpus* c, const float* queries, int64_
                      uint32_t metric, int32_t mode, int64_t budget, float* out_dist,
                      uint32_t* out_ids, int32_t* out_rounds) {
     if (!ctx || !c) return fail(MANS_SEARCH_FAILED, "NULL context or corpus");
+    if (check_k(k) != MANS_OK) return MANS_SEARCH_FAILED;
     if (nq <= 0 || k <= 0) return MANS_OK;
     if (!queries || !out_dist || !out_ids) return fail(MANS_SEARCH_FAILED, "NULL buffer");
     DeviceGuard dg(ctx->device);

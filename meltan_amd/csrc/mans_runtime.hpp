@@ -18,6 +18,13 @@ namespace mans {
 int fail(int code, const std::string& msg);
 int hip_fail(hipError_t e, const char* what);
 
+// Output rows are k slots apart and the kernels index them with a 32-bit
+// stride, so every search entry point rejects a larger k.
+constexpr int64_t kMaxOutputK = 0x7FFFFFFF;
+inline int check_k(int64_t k) {
+    return k > kMaxOutputK ? fail(MANS_SEARCH_FAILED, "k above 2^31 - 1 is not supported") : 0;
+}
+
 struct DevBuf {
     void* p = nullptr;
     size_t bytes = 0;

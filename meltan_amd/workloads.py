@@ -153,6 +153,14 @@ def mixture_10m_96(nq: int = 1024, n: int = 10_000_000):
     return db, q, ctr
 
 
+def mixture_10m_96_train(n: int = 262_144):
+    """The IVF-PQ training sample: 262,144 rows of the same 8,192-centre
+    mixture (seed 5003)."""
+    ctr = centers(5001, 8192, 96)
+    rows, _ = mixture_rows(5003, ctr, 0.25, n, False)
+    return rows
+
+
 # Test-suite generators of the reference, restated (reproducible in C):
 # FlatSearchTests.swift:15-22 and BoundedExactScanTests.swift:23-34.
 

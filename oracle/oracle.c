@@ -754,51 +754,102 @@ ORC_EXPORT int64_t orc_ivf_search(const float *packed, const float *packed_norms
     return topk;
 }
 
-/* Lloyd k-means with strided-sample initialisation, used to make IVF and PQ
- * centroids for the benchmarks and fixtures.  The reference's KMeans
- * (KMeans.swift:53-328) seeds with Swift's stdlib RNG, which cannot be
- * reproduced; this is a deterministic stand-in.  Initial centroids: rows
- * 0, s, 2s, ... with s = max(1, n / k) (the sample rule of
- * IVFFlatSearch.swift:529-543).  Each iteration assigns with orc_ivf_assign
- * semantics, then sets every non-empty centroid to the fp64 mean of its
- * rows taken in ascending row order (empty clusters keep their centroid,
- * KMeans.swift:242-246). */
-ORC_EXPORT void orc_kmeans(const float *rows, int64_t n, int64_t dim, int64_t k, int64_t iters,
-                           int metric, float *centroids, int32_t *assign_out) {
+ORC_EXPORT float orc_simd_distance(const float *a, const float *b, int64_t dim, int metric);
+
+/* KMeans.cluster (KMeans.swift:53-257) over `n` rows of `dim` floats read at
+ * row stride `ld` (a subspace of wider rows when ld > dim, as
+ * clusterSubspace does).  Lloyd loop (KMeans.swift:98-250), single-worker
+ * order:
+ *   - assignment: argmin over centroids of SIMDDistance.distance
+ *     (orc_simd_distance), strict < so the first centroid wins ties
+ *     (KMeans.swift:196-215);
+ *   - stop before the update when no assignment changed (the previous
+ *     assignments start at -1, so the first pass always changes);
+ *   - update: per centroid the Float sum of its rows in row order times
+ *     scale = 1 / Float(count) (KMeans.swift:224-250); empty clusters keep
+ *     their centroid (KMeans.swift:242-246).
+ * The reference seeds with k-means++ drawn from Swift's stdlib RNG
+ * (KMeans.swift:259-328), which is not reproduced: the initial centroids
+ * here are rows 0, s, 2s, ... with s = max(1, n / k).  assign_out
+ * (nullable) receives Result.assignments: those of the last assignment
+ * pass (-1 everywhere when iters == 0).  The multi-worker path of the
+ * reference (KMeans.swift:108-188) adds per-worker partial sums whose split
+ * depends on the core count; this is its single-worker order. */
+ORC_EXPORT void orc_kmeans_ld(const float *rows, int64_t n, int64_t dim, int64_t ld, int64_t k,
+                              int64_t iters, int metric, float *centroids, int32_t *assign_out) {
     int64_t stride = n / k > 1 ? n / k : 1;
     for (int64_t c = 0; c < k; ++c)
-        memcpy(centroids + c * dim, rows + ((c * stride) % n) * dim, sizeof(float) * (size_t)dim);
-    float *rn = (float *)malloc(sizeof(float) * (size_t)n);
-    float *cn = (float *)malloc(sizeof(float) * (size_t)k);
+        memcpy(centroids + c * dim, rows + ((c * stride) % n) * ld, sizeof(float) * (size_t)dim);
     int32_t *assign = (int32_t *)malloc(sizeof(int32_t) * (size_t)n);
-    double *sums = (double *)malloc(sizeof(double) * (size_t)(k * dim));
+    float *sums = (float *)malloc(sizeof(float) * (size_t)(k * dim));
     int64_t *counts = (int64_t *)malloc(sizeof(int64_t) * (size_t)k);
-    orc_row_norms(rows, n, dim, rn);
+    for (int64_t r = 0; r < n; ++r) assign[r] = -1;
     for (int64_t it = 0; it < iters; ++it) {
-        orc_row_norms(centroids, k, dim, cn);
-        orc_ivf_assign(rows, rn, n, dim, centroids, cn, k, metric, assign);
-        memset(sums, 0, sizeof(double) * (size_t)(k * dim));
+        int changed = 0;
+        memset(sums, 0, sizeof(float) * (size_t)(k * dim));
         memset(counts, 0, sizeof(int64_t) * (size_t)k);
         for (int64_t r = 0; r < n; ++r) {
-            int64_t c = assign[r];
-            counts[c]++;
-            for (int64_t d = 0; d < dim; ++d) sums[c * dim + d] += (double)rows[r * dim + d];
+            const float *x = rows + r * ld;
+            int32_t best = 0;
+            float bestd = 3.4028234663852886e38f;
+            for (int64_t c = 0; c < k; ++c) {
+                float d = orc_simd_distance(x, centroids + c * dim, dim, metric);
+                if (d < bestd) {
+                    bestd = d;
+                    best = (int32_t)c;
+                }
+            }
+            if (assign[r] != best) {
+                assign[r] = best;
+                changed = 1;
+            }
+            counts[best]++;
+            for (int64_t d = 0; d < dim; ++d) sums[best * dim + d] += x[d];
         }
+        if (!changed) break;
         for (int64_t c = 0; c < k; ++c) {
             if (counts[c] == 0) continue;
-            for (int64_t d = 0; d < dim; ++d)
-                centroids[c * dim + d] = (float)(sums[c * dim + d] / (double)counts[c]);
+            float scale = 1.0f / (float)counts[c];
+            for (int64_t d = 0; d < dim; ++d) centroids[c * dim + d] = sums[c * dim + d] * scale;
         }
     }
-    if (assign_out) {
-        orc_row_norms(centroids, k, dim, cn);
-        orc_ivf_assign(rows, rn, n, dim, centroids, cn, k, metric, assign_out);
-    }
-    free(rn);
-    free(cn);
+    if (assign_out) memcpy(assign_out, assign, sizeof(int32_t) * (size_t)n);
     free(assign);
     free(sums);
     free(counts);
+}
+
+ORC_EXPORT void orc_kmeans(const float *rows, int64_t n, int64_t dim, int64_t k, int64_t iters,
+                           int metric, float *centroids, int32_t *assign_out) {
+    orc_kmeans_ld(rows, n, dim, dim, k, iters, metric, centroids, assign_out);
+}
+
+/* IVFFlatSearch.buildPartition's training (IVFFlatSearch.swift:517-551):
+ * L = min(max(1, nlist), n) lists; a sample of
+ * min(n, max(L, min(4096, max(16 L, L)))) rows taken at stride
+ * max(1, n / sampleCount) from row 0, topped up with rows
+ * sample.count % n; KMeans.cluster(k = L, maxIterations 8, metric).
+ * Writes L x dim centroids, returns L. */
+ORC_EXPORT int64_t orc_ivf_flat_train(const float *rows, int64_t n, int64_t dim, int64_t nlist,
+                                      int metric, float *centroids) {
+    int64_t lists = nlist < 1 ? 1 : nlist;
+    if (lists > n) lists = n;
+    int64_t sixteen = lists * 16 > lists ? lists * 16 : lists;
+    int64_t cap = 4096 < sixteen ? 4096 : sixteen;
+    int64_t want = lists > cap ? lists : cap;
+    int64_t count = n < want ? n : want;
+    int64_t stride = n / count > 1 ? n / count : 1;
+    float *sample = (float *)malloc(sizeof(float) * (size_t)(count * dim));
+    int64_t have = 0;
+    for (int64_t cursor = 0; have < count && cursor < n; cursor += stride)
+        memcpy(sample + (have++) * dim, rows + cursor * dim, sizeof(float) * (size_t)dim);
+    while (have < count) {
+        memcpy(sample + have * dim, rows + (have % n) * dim, sizeof(float) * (size_t)dim);
+        ++have;
+    }
+    orc_kmeans(sample, count, dim, lists, 8, metric, centroids, NULL);
+    free(sample);
+    return lists;
 }
 
 /* ------------------------------------------------------------------------ */
@@ -892,6 +943,31 @@ ORC_EXPORT void orc_ivfpq_encode_rows(const float *rows, int64_t n, int64_t dim,
         orc_pq_encode(rows + r * dim, coarse + (int64_t)c * dim, codebooks, m, dsub,
                       codes + r * m);
     }
+}
+
+/* _IVFPQIndex.train (IVFPQIndex.swift:54-104): coarse KMeans.cluster
+ * (nlist, iters, metric) on the rows; residual = row - centroid of its
+ * Result.assignments entry, elementwise in Float (IVFPQIndex.swift:366-368);
+ * then ProductQuantizer.train (ProductQuantizer.swift:10-85): for every
+ * subspace s, KMeans.clusterSubspace over the residuals' dims
+ * [s dsub, (s + 1) dsub) with k = 256, L2 and maxIterations iters.
+ * Needs n >= 256, n >= nlist, dim % m == 0 (checked by the caller). */
+ORC_EXPORT void orc_ivfpq_train(const float *rows, int64_t n, int64_t dim, int64_t nlist,
+                                int64_t m, int64_t iters, int metric, float *coarse,
+                                float *codebooks) {
+    int64_t dsub = dim / m;
+    int32_t *assign = (int32_t *)malloc(sizeof(int32_t) * (size_t)n);
+    orc_kmeans(rows, n, dim, nlist, iters, metric, coarse, assign);
+    float *res = (float *)malloc(sizeof(float) * (size_t)(n * dim));
+    for (int64_t r = 0; r < n; ++r) {
+        const float *c = coarse + (int64_t)assign[r] * dim;
+        for (int64_t d = 0; d < dim; ++d) res[r * dim + d] = rows[r * dim + d] - c[d];
+    }
+    for (int64_t s = 0; s < m; ++s)
+        orc_kmeans_ld(res + s * dsub, n, dsub, dim, 256, iters, METRIC_L2,
+                      codebooks + s * 256 * dsub, NULL);
+    free(res);
+    free(assign);
 }
 
 /* distanceTableFlattened (ProductQuantizer.swift:223-253). */

@@ -55,6 +55,10 @@ def lib() -> C.CDLL:
                                      _i64, _i32, _vp, _vp, _vp]
         L.orc_ivf_search.restype = _i64
         L.orc_kmeans.argtypes = [_vp, _i64, _i64, _i64, _i64, _i32, _vp, _vp]
+        L.orc_ivf_flat_train.argtypes = [_vp, _i64, _i64, _i64, _i32, _vp]
+        L.orc_ivf_flat_train.restype = _i64
+        L.orc_ivfpq_train.argtypes = [_vp, _i64, _i64, _i64, _i64, _i64, _i32, _vp, _vp]
+        L.orc_ivfpq_train.restype = None
         L.orc_simd_distance.argtypes = [_vp, _vp, _i64, _i32]
         L.orc_simd_distance.restype = _f
         L.orc_nearest_coarse.argtypes = [_vp, _vp, _i64, _i64, _i32]
@@ -243,6 +247,25 @@ def kmeans(rows, k, iters, metric):
     lib().orc_kmeans(_p(rows), rows.shape[0], rows.shape[1], k, iters, metric, _p(cent),
                      _p(assign))
     return cent, assign
+
+
+def ivf_flat_train(rows, nlist, metric):
+    """buildPartition's sampled k-means: (L x dim centroids)."""
+    rows = _c(rows, np.float32)
+    n, d = rows.shape
+    cent = np.empty((max(1, min(max(1, nlist), n)), d), np.float32)
+    lists = lib().orc_ivf_flat_train(_p(rows), n, d, nlist, metric, _p(cent))
+    return cent[:lists]
+
+
+def ivfpq_train(rows, nlist, m, iters, metric):
+    """_IVFPQIndex.train: (coarse nlist x dim, codebooks m x 256 x dim/m)."""
+    rows = _c(rows, np.float32)
+    n, d = rows.shape
+    coarse = np.empty((nlist, d), np.float32)
+    books = np.empty((m, 256, d // m), np.float32)
+    lib().orc_ivfpq_train(_p(rows), n, d, nlist, m, iters, metric, _p(coarse), _p(books))
+    return coarse, books
 
 
 def simd_distance(a, b, metric):

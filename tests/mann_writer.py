@@ -7,9 +7,25 @@ IDMap payload and the entry point.  Test infrastructure: the files feed the
 loader's parity and corruption tests."""
 from __future__ import annotations
 
+import json
 import struct
 
 import numpy as np
+
+
+def idmap_json(n: int, numeric: int = 0) -> bytes:
+    """An IDMap as JSONEncoder writes it (IDMap.swift:113-120): external ids
+    "e0".."e{n-1}" for the first n - numeric rows, numeric keys for the rest;
+    dictionaries with integer keys are flat arrays of alternating key and
+    value."""
+    named = n - numeric
+    e2i = {f"e{i}": i for i in range(named)}
+    i2e = [x for i in range(named) for x in (i, f"e{i}")]
+    n2i = [x for i in range(named, n) for x in (1000 + i, i)]
+    i2n = [x for i in range(named, n) for x in (i, 1000 + i)]
+    return json.dumps({"externalToInternal": e2i, "internalToExternal": i2e, "nextID": n,
+                       "numericToInternal": n2i, "internalToNumeric": i2n},
+                      separators=(",", ":")).encode()
 
 
 def _pad(buf: bytearray, page: int) -> None:
@@ -17,13 +33,15 @@ def _pad(buf: bytearray, page: int) -> None:
 
 
 def mann_v3_bytes(vectors: np.ndarray, degree: int = 4, metric: int = 0, page: int = 4096,
-                  storage: int | None = None, dim: int | None = None, idmap: bytes = b"{}",
+                  storage: int | None = None, dim: int | None = None, idmap: bytes | None = None,
                   entry_point: int = 0, version: int = 3, magic: bytes = b"MANN") -> bytes:
     n = vectors.shape[0]
     if storage is None:
         storage = {np.dtype(np.float32): 0, np.dtype(np.float16): 1, np.dtype(np.uint8): 2}[vectors.dtype]
     if dim is None:
         dim = vectors.shape[1] * (8 if storage == 2 else 1)
+    if idmap is None:
+        idmap = idmap_json(n)
     buf = bytearray(magic)
     buf += struct.pack("<6I", version, n, degree, dim, metric, storage)
     _pad(buf, page)

@@ -92,16 +92,42 @@ def test_ivf_empty_lists_and_small_k(gpu_ctx):
     c.release()
 
 
-@pytest.mark.parametrize("metric", [L2, COS])
-def test_kmeans_matches_oracle(gpu_ctx, metric):
-    dim, n, k = 32, 4000, 24
-    rows = workloads.lcg_vectors(1, n, dim, seed=631 + metric)
+@pytest.mark.parametrize("metric", [L2, COS, IP])
+@pytest.mark.parametrize("dim", [32, 128, 7])
+def test_kmeans_matches_oracle(gpu_ctx, metric, dim):
+    # KMeans.cluster (KMeans.swift:53-257): first-wins SIMDDistance
+    # assignment, stop at the first unchanged pass, Float sums in row order
+    # times 1 / Float(count), empty clusters kept -- bit for bit, including
+    # runs long enough to settle.
+    n, k = 4000, 24
+    ctr = workloads.centers(630 + dim, 30, dim)
+    rows, _ = workloads.mixture_rows(631 + metric, ctr, 0.4, n, False)
+    rows[n // k] = rows[0]  # two initial centroids coincide: one stays empty
     c = gpu_ctx.upload(rows)
-    for iters in (0, 1, 6):
+    for iters in (0, 1, 6, 200):
         got = c.kmeans(k, iters, metric)
-        ref = oracle.kmeans(rows, k, iters, metric)
-        ref = ref[0] if isinstance(ref, tuple) else ref
+        ref, _ = oracle.kmeans(rows, k, iters, metric)
         assert np.array_equal(got, ref), f"iters {iters}"
+    c.release()
+
+
+@pytest.mark.parametrize("metric", [L2, IP])
+def test_ivf_flat_train_matches_oracle(gpu_ctx, metric):
+    # buildPartition's sample and 8 k-means iterations (IVFFlatSearch.swift:
+    # 517-551): small nlist (a 16 nlist-row sample), nlist >= 4096 (the
+    # sample rows themselves) and nlist above n.
+    rows = workloads.gauss_rows(641, 3 * 4096 + 5, 16, False)
+    c = gpu_ctx.upload(rows)
+    for nlist in (8, 64, 4096):
+        got = c.ivf_flat_train(nlist, metric)
+        want = oracle.ivf_flat_train(rows, nlist, metric)
+        assert np.array_equal(got, want), nlist
+    small = gpu_ctx.upload(rows[:100])
+    got = small.ivf_flat_train(256, metric)
+    assert np.array_equal(got, oracle.ivf_flat_train(rows[:100], 256, metric))
+    if metric == L2:  # every row is its own nearest centroid
+        assert np.array_equal(got, rows[:100])
+    small.release()
     c.release()
 
 
@@ -113,7 +139,7 @@ def test_ivf_mixture_1m_128_properties(gpu_ctx):
     print("ivf 1M x 128 mixture", flush=True)
     db, q = workloads.mixture_1m_128(nq=64)
     c = gpu_ctx.upload(db)
-    cents = c.kmeans(4096, 3, L2)
+    cents = c.ivf_flat_train(4096, L2)  # the reference's sampled build
     ivf = c.ivf_flat_build(cents, L2)
     off, ids = ivf.lists()
     assert off[-1] == db.shape[0] and np.all(np.diff(off) >= 0)

@@ -3,8 +3,10 @@
 The rules follow MmapIndexLoader.load (MmapIndexLoader.swift:38-196): magic,
 version 3 only, metric and storage codes, non-zero node count and degree,
 binary dims divisible by 8, page-aligned sections within the file, the
-trailer's IDMap within the file and the entry point below the node count;
-every failure is ANNSError.corruptFile with the reference's reason.
+trailer's IDMap within the file, an IDMap payload that decodes with as
+many entries as nodes (MmapIndexLoader.swift:174-182) and the entry point
+below the node count; every failure is ANNSError.corruptFile with the
+reference's reason.
 """
 import struct
 
@@ -12,7 +14,7 @@ import numpy as np
 import pytest
 
 import meltan_amd as M
-from mann_writer import mann_v3_bytes
+from mann_writer import idmap_json, mann_v3_bytes
 
 
 def _inspect(tmp_path, data: bytes, page=4096):
@@ -33,7 +35,7 @@ def test_layout_of_a_valid_file(tmp_path, page):
     assert info.adjacency_offset == page * 2
     assert info.distance_offset == page * 3
     assert info.trailer_offset == page * 4
-    assert info.idmap_bytes == 2
+    assert info.idmap_bytes == len(idmap_json(50))
 
 
 def test_f16_and_binary_storage_are_described(tmp_path):
@@ -73,6 +75,39 @@ def test_corrupt_files(tmp_path):
     huge[8:12] = struct.pack("<I", 0xFFFFFFFF)
     huge[16:20] = struct.pack("<I", 0xFFFFFFFF)
     _corrupt(tmp_path, bytes(huge), "Integer overflow")
+
+
+def test_idmap_payload_is_decoded_and_counted(tmp_path):
+    vec = np.ones((6, 4), np.float32)
+    ok = [
+        idmap_json(6),
+        idmap_json(6, numeric=2),  # IDMap.count adds the numeric keys
+        # Optional numeric maps absent or null; unknown keys ignored; the
+        # object form of an integer-keyed dictionary.
+        b'{"externalToInternal":{"a":0,"b":1,"c":2,"d":3,"e":4,"f":5},'
+        b'"internalToExternal":{"0":"a","1":"b"},"nextID":6,"extra":[1,{"x":null}]}',
+        b' {"nextID":6,"internalToExternal":[],"numericToInternal":null,'
+        b'"externalToInternal":{"a\\u0062":0,"b":1,"c":2,"d":3,"e":4,"\\n":5}} ',
+    ]
+    for payload in ok:
+        assert _inspect(tmp_path, mann_v3_bytes(vec, idmap=payload)).node_count == 6
+    corrupt = [
+        b"{}",  # required keys missing
+        b"",
+        b"[]",
+        b'{"externalToInternal":{"a":0},"internalToExternal":[0],"nextID":1}',  # odd array
+        b'{"externalToInternal":{"a":-1},"internalToExternal":[],"nextID":1}',
+        b'{"externalToInternal":{"a":4294967296},"internalToExternal":[],"nextID":1}',
+        b'{"externalToInternal":{"a":1.5},"internalToExternal":[],"nextID":1}',
+        b'{"externalToInternal":{"a":0},"internalToExternal":[],"nextID":1} x',
+        idmap_json(6)[:-1],
+    ]
+    for payload in corrupt:
+        _corrupt(tmp_path, mann_v3_bytes(vec, idmap=payload), "IDMap payload is corrupt")
+    # Decodes, but with fewer (or duplicate) entries than nodes.
+    _corrupt(tmp_path, mann_v3_bytes(vec, idmap=idmap_json(5)), "ID map size does not match node count")
+    dup = b'{"externalToInternal":{"a":0,"a":1,"b":2,"c":3,"d":4,"e":5},"internalToExternal":[],"nextID":6}'
+    _corrupt(tmp_path, mann_v3_bytes(vec, idmap=dup), "ID map size does not match node count")
 
 
 def test_missing_file_is_reported(tmp_path):

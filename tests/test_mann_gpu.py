@@ -13,7 +13,8 @@ import pytest
 import meltan_amd as M
 from meltan_amd import workloads
 from mann_writer import write_mann_v3
-from test_flat_gpu import COS, L2
+from oracle import oracle
+from test_flat_gpu import COS, IP, L2, check_flat
 
 pytestmark = pytest.mark.gpu
 
@@ -39,6 +40,24 @@ def test_mann_upload_equals_memory_upload(gpu_ctx, tmp_path, page):
         assert np.array_equal(a, b)
     fc.release()
     mc.release()
+
+
+@pytest.mark.parametrize("metric", [COS, L2, IP])
+def test_mann_loaded_corpus_matches_the_oracle(gpu_ctx, tmp_path, metric):
+    # The corpus read from the file's vector section searched against the
+    # oracle over the rows that were written: exact top-k, bit for bit.
+    n, dim = 30000, 384
+    rows = workloads.gauss_rows(811, n, dim, True)
+    path = tmp_path / "c.mann"
+    write_mann_v3(path, rows, degree=4, metric=metric, page=16384)
+    fc, got_metric = gpu_ctx.upload_mann(path, 16384)
+    assert got_metric == metric
+    q = workloads.gauss_rows(812, 24, dim, True)
+    norms = oracle.row_norms(rows)
+    for k in (1, 10, 100):
+        gd, gi = fc.flat_search(q, k, metric)
+        check_flat(rows, norms, q, k, metric, gd, gi, f"mann k{k}")
+    fc.release()
 
 
 def test_mann_upload_larger_than_one_staging_chunk(gpu_ctx, tmp_path):

@@ -311,10 +311,125 @@ def test_ivf_lists_are_a_partition():
     for c in range(32):
         seg = ids[off[c]:off[c + 1]]
         assert np.all(assign[seg] == c) and np.all(np.diff(seg.astype(np.int64)) > 0)
-    # each row's list centroid is its nearest (float64 check, ties aside)
-    d = ((corpus[:, None, :].astype(np.float64) - cent[None].astype(np.float64)) ** 2).sum(2)
+    # k-means returns the assignment of its last pass, before that pass's
+    # update (KMeans.swift:253-256); each row's list is its nearest centroid
+    # among the centroids that pass saw (float64 check, ties aside).
+    prev, _ = oracle.kmeans(corpus, 32, 4, L2)
+    d = ((corpus[:, None, :].astype(np.float64) - prev[None].astype(np.float64)) ** 2).sum(2)
     best = d.min(1)
     assert np.all(d[np.arange(5000), assign] <= best + 1e-4)
+
+
+# ---- k-means (KMeans.swift:53-257) -------------------------------------------------
+
+def _seq_mean(rows):
+    """KMeans.swift:224-250: the Float sum in row order times 1 / Float(count)."""
+    acc = np.zeros(rows.shape[1], np.float32)
+    for r in rows:
+        acc = (acc + r).astype(np.float32)
+    return (acc * (np.float32(1.0) / np.float32(len(rows)))).astype(np.float32)
+
+
+def _dist64(rows, cent, metric):
+    a, b = rows.astype(np.float64), cent.astype(np.float64)
+    if metric == L2:
+        return ((a[:, None, :] - b[None]) ** 2).sum(2)
+    dot = a @ b.T
+    if metric == IP:
+        return -dot
+    return 1.0 - dot / (np.linalg.norm(a, axis=1)[:, None] * np.linalg.norm(b, axis=1)[None])
+
+
+@pytest.mark.parametrize("metric", [L2, IP, COS])
+def test_kmeans_update_is_the_float_mean_of_the_previous_assignment(metric):
+    n, k = 3000, 20
+    rows = workloads.gauss_rows(41, n, 12, False)
+    init, a0 = oracle.kmeans(rows, k, 0, metric)
+    assert np.all(a0 == -1)  # Result.assignments before any pass
+    assert np.array_equal(init, rows[(np.arange(k) * (n // k)) % n])
+    c1, a1 = oracle.kmeans(rows, k, 1, metric)
+    d = _dist64(rows, init, metric)
+    assert np.all(d[np.arange(n), a1] <= d.min(1) + 1e-5 * (1 + np.abs(d.min(1))))
+    for c in range(k):
+        members = rows[a1 == c]
+        if len(members) == 0:
+            assert np.array_equal(c1[c], init[c])
+        else:
+            assert np.array_equal(c1[c], _seq_mean(members)), c
+
+
+def test_kmeans_returns_the_last_pass_and_stops_when_settled():
+    n, k = 4000, 16
+    ctr = workloads.centers(45, 16, 8)
+    rows = workloads.mixture_rows(46, ctr, 0.3, n, False)[0]
+    for t in (2, 3, 5):
+        before, _ = oracle.kmeans(rows, k, t - 1, L2)
+        _, at = oracle.kmeans(rows, k, t, L2)
+        assert np.array_equal(at, _dist64(rows, before, L2).argmin(1))
+    # Once a pass changes nothing the loop stops: more iterations change nothing.
+    settled = None
+    for t in range(2, 60):
+        a, _ = oracle.kmeans(rows, k, t, L2)
+        b, _ = oracle.kmeans(rows, k, t + 1, L2)
+        if np.array_equal(a, b):
+            settled = t
+            break
+    assert settled is not None
+    c_many, a_many = oracle.kmeans(rows, k, 500, L2)
+    c_set, _ = oracle.kmeans(rows, k, settled, L2)
+    assert np.array_equal(c_many, c_set)
+    assert np.array_equal(a_many, _dist64(rows, c_many, L2).argmin(1))
+
+
+def test_kmeans_ties_go_to_the_first_centroid_and_empty_clusters_keep_theirs():
+    n, k = 1000, 10
+    rows = workloads.gauss_rows(47, n, 6, False)
+    rows[n // k] = rows[0]  # initial centroids 0 and 1 coincide
+    c, a = oracle.kmeans(rows, k, 1, L2)
+    assert not np.any(a == 1) and a[n // k] == 0
+    assert np.array_equal(c[1], rows[0])
+
+
+def test_ivf_flat_train_uses_the_reference_sample():
+    # IVFFlatSearch.swift:528-551.  With L >= 4096 the sample holds exactly L
+    # rows at stride n // L; k-means with k equal to the sample size leaves
+    # every (distinct) sample row as its own centroid.
+    n = 3 * 4096 + 5
+    rows = workloads.gauss_rows(48, n, 4, False)
+    cent = oracle.ivf_flat_train(rows, 4096, L2)
+    assert np.array_equal(cent, rows[0:3 * 4096:3])
+    # Fewer rows than lists: L = n and every row is a centroid.
+    cent = oracle.ivf_flat_train(rows[:100], 256, L2)
+    assert np.array_equal(cent, rows[:100])
+    # Small nlist: min(n, max(L, min(4096, 16 L))) rows at stride n // count,
+    # clustered with 8 iterations.
+    want, _ = oracle.kmeans(rows[0:n:n // 128][:128], 8, 8, IP)
+    assert np.array_equal(oracle.ivf_flat_train(rows, 8, IP), want)
+
+
+def test_ivfpq_train_closed_form_and_composition():
+    # IVFPQIndex.swift:54-104, ProductQuantizer.swift:10-85.  With one coarse
+    # list the centroid is the mean of all rows; with 256 rows every
+    # codebook is the residuals' subvectors themselves.
+    rng = np.random.default_rng(49)
+    rows = rng.standard_normal((256, 16)).astype(np.float32)
+    for metric in (L2, IP):
+        coarse, books = oracle.ivfpq_train(rows, 1, 4, 5, metric)
+        mean = _seq_mean(rows)
+        assert np.array_equal(coarse[0], mean)
+        res = (rows - mean).astype(np.float32)
+        for sub in range(4):
+            assert np.array_equal(books[sub], res[:, 4 * sub:4 * sub + 4])
+    # Larger: coarse = k-means of the rows; codebooks = k-means of the
+    # residual subvectors against the last pass's assignment.
+    rows = workloads.gauss_rows(50, 1500, 12, False)
+    coarse, books = oracle.ivfpq_train(rows, 6, 3, 4, IP)
+    want_c, assign = oracle.kmeans(rows, 6, 4, IP)
+    assert np.array_equal(coarse, want_c)
+    res = (rows - want_c[assign]).astype(np.float32)
+    for sub in range(3):
+        want_b, _ = oracle.kmeans(np.ascontiguousarray(res[:, 4 * sub:4 * sub + 4]), 256, 4, L2)
+        assert np.array_equal(books[sub], want_b)
 
 
 # ---- PQ ----------------------------------------------------------------------------
@@ -356,3 +471,69 @@ def test_ivfpq_probe_newest_first_ties():
     probes, dist = oracle.ivfpq_probe(coarse, q, 3, L2)
     # centroids 0 and 2 tie; the later index ranks first (BoundedSelection.swift:199-213)
     assert probes.tolist() == [2, 0, 1]
+
+
+def test_ivfpq_search_is_the_sorted_list_over_probed_adc_scores():
+    """_IVFPQIndex.search (IVFPQIndex.swift:177-226) composed from its
+    parts, computed here independently: probes in BoundedSortedList order,
+    per probe the residual LUT, each row's score the Float sum of its m LUT
+    entries in code order, all candidates inserted in arrival order into
+    BoundedSortedList(k).  Duplicate rows make ties at every k."""
+    rng = np.random.default_rng(51)
+    n, dim, m, nlist = 700, 8, 4, 6
+    rows = rng.standard_normal((n, dim)).astype(np.float32)
+    rows[100:160] = rows[7]
+    coarse = rows[[0, 50, 200, 300, 400, 500]].copy()
+    books = rng.standard_normal((m, 256, dim // m)).astype(np.float32)
+    norms = oracle.row_norms(rows)
+    for metric in (L2, IP, COS):
+        assign, codes = oracle.pq_encode_rows(rows, coarse, books, metric)
+        off, ids = oracle.ivf_lists(assign, nlist)
+        for qi in range(4):
+            q = rows[7] if qi == 0 else rng.standard_normal(dim).astype(np.float32)
+            for k, nprobe in ((5, 2), (30, 3), (64, 6)):
+                got_s, got_i = oracle.ivfpq_search(coarse, books, codes, off, ids, metric, q, k,
+                                                   nprobe)
+                probes, _ = oracle.ivfpq_probe(coarse, q, nprobe, metric)
+                cs, ci = [], []
+                for p in probes:
+                    lut = oracle.pq_lut((q - coarse[p]).astype(np.float32), books, metric)
+                    members = ids[off[p]:off[p + 1]]
+                    sc = np.zeros(len(members), np.float32)
+                    for sub in range(m):
+                        sc = (sc + lut[sub, codes[members, sub]]).astype(np.float32)
+                    cs.append(sc)
+                    ci.append(members)
+                cs, ci = np.concatenate(cs), np.concatenate(ci)
+                want_s, want_i = oracle.sorted_list_run(cs, ci, k)
+                assert got_i.tolist() == want_i.tolist() and np.array_equal(got_s, want_s)
+                # No candidate left out scores below the kept ones; equal
+                # scores come newest first.
+                assert np.all(cs[~np.isin(ci, want_i)] >= want_s[-1])
+                pos = {int(i): j for j, i in enumerate(ci)}
+                for a in range(len(want_i) - 1):
+                    if want_s[a] == want_s[a + 1]:
+                        assert pos[int(want_i[a])] > pos[int(want_i[a + 1])]
+                # The exact rerank: the kept ids' host distances, (distance, id) order.
+                rk = min(5, k)
+                rs, ri = oracle.ivfpq_search(coarse, books, codes, off, ids, metric, q, k, nprobe,
+                                             rows=rows, rerank_k=rk)
+                exact = oracle.distances_for_ids(rows, norms, q, want_i, metric)
+                order = np.lexsort((want_i, exact))[:rk]
+                assert ri.tolist() == want_i[order].tolist() and np.array_equal(rs, exact[order])
+
+
+@pytest.mark.parametrize("metric", [COS, L2, IP])
+def test_int8_fixed_budget_over_every_row_is_the_exact_result(metric):
+    """Mode 1 with budget = n selects every row, so the rescored top-k is
+    the exact fp32 scan's (BoundedExactScan.swift:96-122, 320-369)."""
+    n, dim = 16384 + 256, 48
+    corpus = workloads.lcg_vectors(1, n, dim, seed=31)
+    planes = oracle.int8_build(corpus)
+    norms = oracle.row_norms(corpus)
+    for sd in range(3):
+        q = workloads.lcg_vectors(1, 1, dim, seed=310 + sd)[0]
+        d, ids, _ = oracle.int8_search(corpus, norms, planes, q, 10, metric, cores=8, mode=1,
+                                       budget=n)
+        fd, fi = oracle.flat_search(corpus, norms, q, 10, metric, cores=8)
+        assert np.array_equal(d, fd) and ids.tolist() == fi.tolist()
