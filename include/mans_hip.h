@@ -141,6 +141,22 @@ int mans_flat_search_device(mans_ctx *ctx, const mans_corpus *corpus, const floa
                             int64_t nq, int64_t k, uint32_t metric, float *d_out_dist,
                             uint32_t *d_out_ids, void *stream);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): mans_flat_search_device's results (its streaming scan
+ * and proof loop) with every workspace taken from a fixed device array of
+ * MANS_NOALLOC_SCRATCH_BYTES that each GPU holds until the process ends.
+ * Calls no hipMalloc/hipFree or allocating library routine; work runs on
+ * `stream` (NULL: the null stream) and the call blocks until done.  Queries
+ * go through in rounds sized to the array; a corpus for which one query's
+ * workspace does not fit gives MANS_RESOURCE_EXHAUSTED.  Calls on one GPU
+ * share the array (it keeps the last call's contents) and are serialised by
+ * a per-device lock. */
+#define MANS_NOALLOC_SCRATCH_BYTES (16 * 1024 * 1024)
+int mans_flat_search_device_noalloc(mans_ctx *ctx, const mans_corpus *corpus,
+                                    const float *d_queries, int64_t nq, int64_t k, uint32_t metric,
+                                    float *d_out_dist, uint32_t *d_out_ids, void *stream);
+
 /* int8 prefilter + fp32 rerank: BoundedExactScan.search
  * (BoundedExactScan.swift:30-122).  mode 0: adaptive budget with the
  * reference's lower-bound proof (results are exact); mode 1: one round at

@@ -51,6 +51,7 @@ EXPORTS = [
     "mans_last_error", "mans_ctx_create", "mans_ctx_destroy", "mans_corpus_upload_f32",
     "mans_mann_inspect", "mans_corpus_upload_mann", "mans_corpus_write_rows", "mans_corpus_invalidate", "mans_corpus_release",
     "mans_corpus_count", "mans_corpus_dim", "mans_flat_search", "mans_flat_search_device",
+    "mans_flat_search_device_noalloc",
     "mans_int8_search", "mans_int8_search_device", "mans_int8_codes_download",
     "mans_ivf_flat_build", "mans_kmeans", "mans_ivf_flat_train", "mans_ivf_flat_search",
     "mans_ivf_flat_search_device", "mans_ivf_download_lists", "mans_ivf_release",
@@ -59,6 +60,8 @@ EXPORTS = [
     "mans_ivfpq_release",
     "mans_timing_enable", "mans_timing_read", "mans_timing_reset",
 ]
+
+NOALLOC_SCRATCH_BYTES = 16 * 1024 * 1024  # MANS_NOALLOC_SCRATCH_BYTES
 
 
 class ANNSError(RuntimeError):
@@ -120,6 +123,8 @@ def lib() -> C.CDLL:
         L.mans_corpus_dim.restype = _i64
         L.mans_flat_search.argtypes = [_vp, _vp, _vp, _i64, _i64, _u32, _vp, _vp]
         L.mans_flat_search_device.argtypes = [_vp, _vp, _vp, _i64, _i64, _u32, _vp, _vp, _vp]
+        L.mans_flat_search_device_noalloc.argtypes = [_vp, _vp, _vp, _i64, _i64, _u32, _vp, _vp,
+                                                      _vp]
         L.mans_int8_search.argtypes = [_vp, _vp, _vp, _i64, _i64, _u32, _i32, _i64, _vp, _vp, _vp]
         L.mans_int8_search_device.argtypes = [_vp, _vp, _vp, _i64, _i64, _u32, _i32, _i64, _vp,
                                               _vp, _vp]
@@ -279,6 +284,14 @@ class Corpus:
                            d_ids: int, stream: int | None = None) -> None:
         _check(lib().mans_flat_search_device(self.ctx.handle, self.handle, d_queries, nq, k,
                                              metric_code(metric), d_dist, d_ids, stream))
+
+    def flat_search_device_noalloc(self, d_queries: int, nq: int, k: int, metric, d_dist: int,
+                                   d_ids: int, stream: int | None = None) -> None:
+        """mans_flat_search_device_noalloc: the same results with no device
+        allocation (workspace in the library's fixed scratch array)."""
+        _check(lib().mans_flat_search_device_noalloc(self.ctx.handle, self.handle, d_queries, nq,
+                                                     k, metric_code(metric), d_dist, d_ids,
+                                                     stream))
 
     def int8_search(self, queries, k: int, metric="cosine", mode: int = 0, budget: int = 0):
         q = _f32(queries, self.dim)

@@ -170,6 +170,8 @@ int mans_ctx_create(int device, mans_ctx** out) {
         delete c;
         return fail(MANS_DEVICE_NOT_SUPPORTED, "HIP runtime initialisation failed");
     }
+    // A failure here only disables mans_flat_search_device_noalloc.
+    (void)noalloc_init(device);
     *out = c;
     return MANS_OK;
 }

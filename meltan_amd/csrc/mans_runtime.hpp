@@ -128,5 +128,8 @@ int flat_search_run(mans_ctx* ctx, const mans_corpus* c, const float* d_q, int64
                     uint32_t metric, float* d_dist, uint32_t* d_ids, hipStream_t st, Slot* slot,
                     float* h_dist, uint32_t* h_ids);
 hipError_t int8_refresh_rows(mans_corpus* c, int64_t first_row, int64_t count, hipStream_t s);
+// Takes the no-allocation scratch array's device address on `device`
+// (current); called once per device when a context is created.
+int noalloc_init(int device);
 
 }  // namespace mans
