@@ -14,8 +14,11 @@ Every workload first checks a sample of queries against the CPU oracle
 (bit-identical results) and stops if they differ.  Throughput is timed with
 no per-kernel synchronisation; kernel durations for the roofline come from
 a separate pass with HIP events recorded on the stream the kernels run on.
-The CPU baseline (the oracle's restatement of the reference CPU path) is
-timed on a bounded sample on the host's cores in the same run.
+The CPU baseline of each line is the oracle's restatement of the route the
+reference's CPU path takes for that configuration (no GPU context:
+FlatGPUSearch.swift:63-94, 754-779, 1003-1037), timed on a bounded sample on
+this host's cores in the same run; each baseline records the CPU model,
+nproc, NUMA layout and the threads it used.
 """
 from __future__ import annotations
 
@@ -36,7 +39,42 @@ HBM_PEAK_GBS = 8000.0
 FP32_MFMA_TFLOPS = 157.3
 BF16_MFMA_TFLOPS = 2500.0  # dense
 METRIC = "queries/sec exact top-10 @1M×384 fp32 (batch 1/1024); p50 single-query µs @100k"
-CPU_THREADS = min(16, os.cpu_count() or 1)  # the host share of one GPU
+CPU_THREADS = min(16, os.cpu_count() or 1)  # the host's CPU share of one GPU
+
+
+def host_info() -> dict:
+    """CPU model, logical CPUs, NUMA nodes and the threads a baseline uses."""
+    model = None
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    numa = []
+    for node in sorted(Path("/sys/devices/system/node").glob("node[0-9]*")):
+        try:
+            numa.append(f"{node.name}: cpus {(node / 'cpulist').read_text().strip()}")
+        except OSError:
+            pass
+    return {"cpu_model": model, "nproc": os.cpu_count(), "numa": numa,
+            "threads_used": CPU_THREADS,
+            "note": "worker threads sized to the CPU share of one GPU on this host (16)"}
+
+
+def cpu_line(value, unit, cores, sample, kind="port"):
+    return {"value": round(value, 2), "unit": unit, "cores": cores, "kind": kind, "sample": sample,
+            "host": host_info()}
+
+
+def sha(*arrays) -> str:
+    import hashlib
+
+    h = hashlib.sha256()
+    for a in arrays:
+        h.update(np.ascontiguousarray(a).tobytes())
+    return h.hexdigest()
 
 
 def log(msg: str) -> None:
@@ -136,6 +174,7 @@ def bench_flat(args, ctx):
     log(f"flat: generating {n} x {dim} mixture corpus")
     nq_pool = max(1024, B)
     db, q = workloads.mixture_1m_384(nq=nq_pool, n=n)
+    data_sha = sha(db, q)
     corpus = ctx.upload(db)
     norms = oracle.row_norms(db)
     gd, gi = corpus.flat_search(q[:8], k, metric)
@@ -192,40 +231,38 @@ def bench_flat(args, ctx):
 
     extra = {}
     if not args.quick:
-        # C2: p50 single-query latency at 100k x 384 through the host-pointer C ABI.
-        db100, q100 = workloads.flat_100k(1024)
-        c100 = ctx.upload(db100)
-        gd, gi = c100.flat_search(q100[:4], k, metric)
-        parity_flat(db100, oracle.row_norms(db100), q100[:4], gd, gi, k, metric)
-        for i in range(50):
-            c100.flat_search(q100[i:i + 1], k, metric)
-        lat = []
-        for i in range(1000):
-            t = time.perf_counter()
-            c100.flat_search(q100[i % 1024:i % 1024 + 1], k, metric)
-            lat.append((time.perf_counter() - t) * 1e6)
-        extra["p50_us_100k"] = round(percentile_nearest_rank(lat, 0.5), 2)
-        extra["p95_us_100k"] = round(percentile_nearest_rank(lat, 0.95), 2)
-        for b in (32, 1024):
-            t = time.perf_counter()
-            reps = 10
-            for r in range(reps):
-                c100.flat_search(q100[:b], k, metric)
-            extra[f"qps_100k_batch{b}_host_api"] = round(b * reps / (time.perf_counter() - t), 1)
-        c100.release()
+        extra["c1"] = bench_single_queries(args, ctx, "c1")
+        extra["c2"] = bench_single_queries(args, ctx, "c2")
 
-    cpu = None
+    cpu = cpu1 = None
     if not args.no_cpu:
+        # T2: a batch without a GPU context goes query by query through
+        # HostBatchWork.run -- the int8 bounded scan, mode 0, at n >= 16384
+        # (FlatGPUSearch.swift:1024-1036) -- across the cores.
         nsample = args.cpu_queries
-        log(f"flat: CPU baseline on {nsample} queries, {CPU_THREADS} threads")
+        log(f"flat: CPU baseline (host batch route) on {nsample} queries, {CPU_THREADS} threads")
+        planes = oracle.int8_build(db)
         t0 = time.perf_counter()
-        oracle.flat_search_batch(db, norms, q[:nsample], k, metric, threads=CPU_THREADS)
+        _, _, _, route = oracle.host_batch_search(db, norms, planes, q[:nsample], k, metric,
+                                                  cores=CPU_THREADS, threads=CPU_THREADS)
         dt = time.perf_counter() - t0
-        cpu = {"value": round(nsample / dt, 2), "unit": "queries/s", "cores": CPU_THREADS,
-               "kind": "port",
-               "sample": (f"{nsample} queries, exact top-{k} cosine over the same {n}x{dim} corpus, "
-                          f"one query per thread (FlatGPUSearch.swift:754-779), scalar dots.c "
-                          f"order, {dt:.2f} s")}
+        del planes
+        cpu = cpu_line(nsample / dt, "queries/s", CPU_THREADS,
+                       f"{nsample} queries of the same batch workload through HostBatchWork.run "
+                       f"(FlatGPUSearch.swift:1003-1037): {int(route.sum())} took the int8 "
+                       f"BoundedExactScan (mode 0, adaptive and proven exact), one query per "
+                       f"thread; {dt:.2f} s")
+        # T1: one query alone, n > 40960 and no GPU: the fp32
+        # ParallelFlatScan with min(cores, 32, n / 2048) slices on the cores.
+        nq1 = 24
+        t0 = time.perf_counter()
+        for i in range(nq1):
+            oracle.flat_search(db, norms, q[i], k, metric, cores=CPU_THREADS, threads=CPU_THREADS)
+        dt = time.perf_counter() - t0
+        cpu1 = cpu_line(nq1 / dt, "queries/s", CPU_THREADS,
+                        f"{nq1} single queries through ParallelFlatScan.search "
+                        f"({min(CPU_THREADS, 32, n // 2048)} slices, FlatGPUSearch.swift:63-94), "
+                        f"{dt:.2f} s")
     corpus.release()
     main_b = res[B]
     out = {
@@ -246,9 +283,99 @@ def bench_flat(args, ctx):
         "roofline": main_b["roofline"],
         "cpu_baseline": cpu,
         "batch1": {"qps": round(res[1]["qps"], 2), "ms_per_query": round(res[1]["ms_per_step"], 4),
-                   "roofline": res[1]["roofline"]},
+                   "roofline": res[1]["roofline"], "cpu_baseline": cpu1},
+        "data_sha256": {"corpus+queries": data_sha},
     }
     out.update(extra)
+    if "c2" in extra:  # the metric's single-query latency at 100k, end to end
+        out["p50_us_100k"] = extra["c2"]["p50_us"]
+        out["p95_us_100k"] = extra["c2"]["p95_us"]
+        out["kernel_p50_us_100k"] = extra["c2"]["kernel_p50_us"]
+    return out
+
+
+def bench_single_queries(args, ctx, which):
+    """C1 (10,000 x 384) or C2 (100,000 x 384): exact cosine top-10, one
+    query per call.  p50/p95 through the host-pointer C ABI (query upload,
+    kernels, results back: PCIe included), the kernel-only p50 (HIP events
+    around the scan and its merge, on their stream), and for C2 the batch-32
+    and batch-1024 host-API throughput; the CPU baseline is the reference's
+    single-query host route on this host."""
+    import meltan_amd as M
+    from meltan_amd import workloads
+    from oracle import oracle
+
+    k, metric = 10, M.METRIC_COSINE
+    if which == "c1":
+        db, q = workloads.flat_10k(1000)
+        desc = "exact flat top-10 cosine, 10000x384, batch 1"
+    else:
+        db, q = workloads.flat_100k(1024)
+        desc = "exact flat top-10 cosine, 100000x384, batch 1 (also 32, 1024)"
+    n = db.shape[0]
+    c = ctx.upload(db)
+    norms = oracle.row_norms(db)
+    gd, gi = c.flat_search(q[:4], k, metric)
+    parity_flat(db, norms, q[:4], gd, gi, k, metric)
+    for i in range(50):
+        c.flat_search(q[i:i + 1], k, metric)
+    lat = []
+    t_all = time.perf_counter()
+    for i in range(1000):
+        t = time.perf_counter()
+        c.flat_search(q[i % q.shape[0]:i % q.shape[0] + 1], k, metric)
+        lat.append((time.perf_counter() - t) * 1e6)
+    t_all = time.perf_counter() - t_all
+    kern = []
+    ctx.timing(True)
+    for i in range(300):
+        ctx.timing_reset()
+        c.flat_search(q[i % q.shape[0]:i % q.shape[0] + 1], k, metric)
+        ms, cnt = ctx.timing_read("flat_scan")
+        if cnt:
+            kern.append(ms * 1e3)
+    ctx.timing(False)
+    p50k = percentile_nearest_rank(kern, 0.5)
+    out = {"workload": desc,
+           "p50_us": round(percentile_nearest_rank(lat, 0.5), 2),
+           "p95_us": round(percentile_nearest_rank(lat, 0.95), 2),
+           "qps_host_api": round(1000 / t_all, 1),
+           "kernel_p50_us": round(p50k, 2),
+           "kernel_roofline": roofline_hbm("flat_scan_f4<6> + flat_fast_merge<6>",
+                                           f"flat_{n}x384_b1", n * (384 * 4 + 4), p50k / 1e6),
+           "data_sha256": sha(db, q)}
+    if which == "c2":
+        for b in (32, 1024):
+            t = time.perf_counter()
+            reps = 10
+            for r in range(reps):
+                c.flat_search(q[:b], k, metric)
+            out[f"qps_batch{b}_host_api"] = round(b * reps / (time.perf_counter() - t), 1)
+    if not args.no_cpu:
+        # A single query without a GPU context: n < 16384 or n > 40960 takes
+        # the fp32 ParallelFlatScan with min(cores, 32, n / 2048) slices
+        # (FlatGPUSearch.swift:63-94).
+        slices = max(1, min(CPU_THREADS, 32, n // 2048))
+        lat_cpu = []
+        for i in range(100 if which == "c1" else 40):
+            t = time.perf_counter()
+            oracle.flat_search(db, norms, q[i], k, metric, cores=CPU_THREADS, threads=slices)
+            lat_cpu.append((time.perf_counter() - t) * 1e6)
+        out["cpu_baseline"] = cpu_line(
+            percentile_nearest_rank(lat_cpu, 0.5), "us p50 per query", slices,
+            f"{len(lat_cpu)} single queries through ParallelFlatScan.search, {slices} slices "
+            f"on {slices} threads, p50 by nearest rank (LatencyDistribution.swift:154-160)")
+        if which == "c2":
+            planes = oracle.int8_build(db)
+            t0 = time.perf_counter()
+            oracle.host_batch_search(db, norms, planes, q[:256], k, metric, cores=CPU_THREADS,
+                                     threads=CPU_THREADS)
+            out["cpu_baseline_batch"] = cpu_line(
+                256 / (time.perf_counter() - t0), "queries/s", CPU_THREADS,
+                "256 queries through HostBatchWork.run (int8 BoundedExactScan, mode 0, at "
+                "n >= 16384), one query per thread")
+    log(f"{which}: p50 {out['p50_us']} us (kernels {out['kernel_p50_us']} us)")
+    c.release()
     return out
 
 
@@ -257,6 +384,10 @@ def bench_flat(args, ctx):
 # ---------------------------------------------------------------------------
 
 def bench_int8(args, ctx):
+    """C3: the int8 prefilter + fp32 rerank at 1M x 384, batch 1 and 1024,
+    in both modes: mode 1 (the configuration's literal form: top-100 by the
+    int8 keys, then the exact top-10 of those) and mode 0 (the reference's
+    BoundedExactScan: adaptive budget with the lower-bound proof, exact)."""
     import meltan_amd as M
     from meltan_amd import hip, workloads
     from oracle import oracle
@@ -268,48 +399,81 @@ def bench_int8(args, ctx):
     corpus = ctx.upload(db)
     norms = oracle.row_norms(db)
     planes = oracle.int8_build(db)
-    gd, gi, _ = corpus.int8_search(q[:2], k, metric, mode=1, budget=budget)   # threshold collect
-    bd, bi, _ = corpus.int8_search(q[:64], k, metric, mode=1, budget=budget)  # i8 MFMA batch
-    for i in range(2):
-        od, oi, _ = oracle.int8_search(db, norms, planes, q[i], k, metric, mode=1, budget=budget)
-        for rd, ri in ((gd, gi), (bd, bi)):
-            if not (np.array_equal(rd[i, :len(od)], od) and np.array_equal(ri[i, :len(oi)], oi)):
-                raise SystemExit("int8 parity gate failed")
+    for mode in (1, 0):
+        gd, gi, _ = corpus.int8_search(q[:2], k, metric, mode=mode, budget=budget)
+        bd, bi, _ = corpus.int8_search(q[:64], k, metric, mode=mode, budget=budget)
+        for i in range(2):
+            od, oi, _ = oracle.int8_search(db, norms, planes, q[i], k, metric, cores=CPU_THREADS,
+                                           mode=mode, budget=budget)
+            for rd, ri in ((gd, gi), (bd, bi)):
+                if not np.array_equal(rd[i, :len(od)], od):
+                    raise SystemExit(f"int8 parity gate failed (mode {mode})")
+                if mode == 1 and not np.array_equal(ri[i, :len(oi)], oi):
+                    raise SystemExit("int8 parity gate failed (mode 1 ids)")
+    cpu = {}
+    if not args.no_cpu:
+        # The reference's CPU int8 path is BoundedExactScan (mode 0); the
+        # oracle's restatement scans a query on one thread.
+        t0 = time.perf_counter()
+        for i in range(8):
+            oracle.int8_search(db, norms, planes, q[i], k, metric, cores=CPU_THREADS, mode=0)
+        dt = time.perf_counter() - t0
+        cpu[1] = cpu_line(8 / dt, "queries/s", 1,
+                          f"8 single queries through BoundedExactScan.search (mode 0) restated, "
+                          f"one thread per query, {dt:.2f} s")
+        t0 = time.perf_counter()
+        oracle.host_batch_search(db, norms, planes, q[:128], k, metric, cores=CPU_THREADS,
+                                 threads=CPU_THREADS)
+        dt = time.perf_counter() - t0
+        cpu[1024] = cpu_line(128 / dt, "queries/s", CPU_THREADS,
+                             f"128 queries through HostBatchWork.run (BoundedExactScan, mode 0), "
+                             f"one query per thread, {dt:.2f} s")
     del planes
     dq = hip.DeviceArray.from_numpy(q)
     dd = hip.DeviceArray((1024, k), np.float32)
     di = hip.DeviceArray((1024, k), np.uint32)
     stream = hip.Stream()
-    out = {"workload": f"int8 prefilter top-{budget} + exact rerank top-{k}, cosine, {n}x{dim}"}
-    for b, steps in ((1, 100), (1024, 10)):
-        def step(s, b=b):
-            off = (s * b) % (1024 - b + 1)
-            corpus.int8_search_device(dq.offset(off * dim), b, k, metric, 1, budget,
-                                      dd.offset(off * k), di.offset(off * k), stream.handle)
-        elapsed = timed(step, steps, 2, hip)
-        kt = kernel_avg(ctx, step, min(steps, 10), ["int8_scan", "int8_bound", "int8_gemm", "int8_merge"], hip)
-        if b == 1:
-            # The collect launch streams every row's codes and planes once;
-            # the bound launch before it reads a sixteenth of them.
-            avg, launches = kt["int8_scan"]
-            per = b * min(steps, 10) // max(launches, 1)
-            roof = roofline_hbm("int8_collect<6>", f"int8_{n}x{dim}_b{b}", per * n * (dim + 12), avg)
-            roof["bound_pass_us"] = round(kt["int8_bound"][0] * 1e6, 2) if kt["int8_bound"][1] else None
-        else:
-            # The batch is a 1024 x 1e6 x 384 int8 contraction on i8 MFMA
-            # (dense peak 5.0 POP/s) with the key epilogue fused into it.
-            avg, launches = kt["int8_gemm"]
-            ops = 2.0 * b * n * dim
-            roof = {"bound": "mfma", "achieved": round(ops / avg / 1e12, 2), "peak": 5000.0,
-                    "unit": "TOP/s", "frac": round(ops / avg / 1e12 / 5000.0, 5),
-                    "traffic": measured_traffic("int8_gemm<12>", f"int8_{n}x{dim}_b{b}"),
-                    "kernel": "int8_gemm<12,cosine,bounded>", "avg_launch_us": round(avg * 1e6, 2),
-                    "ops_per_launch": int(ops),
-                    "bound_pass_us": round(kt["int8_bound"][0] * 1e6, 2) if kt["int8_bound"][1] else None,
-                    "merge_avg_us": round(kt["int8_merge"][0] * 1e6, 2) if kt["int8_merge"][1] else None,
-                    "reselect_scan_launches": kt["int8_scan"][1]}
-        out[f"batch{b}"] = {"qps": round(b * steps / elapsed, 1), "roofline": roof}
-        log(f"int8: batch {b}: {out[f'batch{b}']['qps']} queries/s")
+    out = {"workload": f"int8 prefilter top-{budget} + exact rerank top-{k}, cosine, {n}x{dim}",
+           "data_sha256": sha(db, q)}
+    for mode in (1, 0):
+        for b, steps in ((1, 100), (1024, 10)):
+            def step(s, b=b, mode=mode):
+                off = (s * b) % (1024 - b + 1)
+                corpus.int8_search_device(dq.offset(off * dim), b, k, metric, mode, budget,
+                                          dd.offset(off * k), di.offset(off * k), stream.handle)
+            elapsed = timed(step, steps, 2, hip)
+            kt = kernel_avg(ctx, step, min(steps, 10),
+                            ["int8_scan", "int8_bound", "int8_gemm", "int8_merge"], hip)
+            if (b == 1 and not kt["int8_scan"][1]) or (b > 1 and not kt["int8_gemm"][1]):
+                roof = None
+            elif b == 1:
+                # The collect launch streams every row's codes and planes once;
+                # the bound launch before it reads a sixteenth of them.
+                # Bytes of one launch: every row's codes and planes (a
+                # mode-0 query may take several launches, one per round).
+                avg, launches = kt["int8_scan"]
+                roof = roofline_hbm("int8_collect<6>", f"int8_{n}x{dim}_b{b}", n * (dim + 12), avg)
+                roof["launches_per_query"] = round(launches / min(steps, 10), 2)
+                roof["bound_pass_us"] = round(kt["int8_bound"][0] * 1e6, 2) if kt["int8_bound"][1] else None
+            else:
+                # The batch is a 1024 x 1e6 x 384 int8 contraction on i8 MFMA
+                # (dense peak 5.0 POP/s) with the key epilogue fused into it.
+                avg, launches = kt["int8_gemm"]
+                ops = 2.0 * b * n * dim
+                roof = {"bound": "mfma", "achieved": round(ops / avg / 1e12, 2), "peak": 5000.0,
+                        "unit": "TOP/s", "frac": round(ops / avg / 1e12 / 5000.0, 5),
+                        "traffic": measured_traffic("int8_gemm<12>", f"int8_{n}x{dim}_b{b}"),
+                        "kernel": "int8_gemm<12,cosine,bounded>", "avg_launch_us": round(avg * 1e6, 2),
+                        "ops_per_launch": int(ops),
+                        "bound_pass_us": round(kt["int8_bound"][0] * 1e6, 2) if kt["int8_bound"][1] else None,
+                        "merge_avg_us": round(kt["int8_merge"][0] * 1e6, 2) if kt["int8_merge"][1] else None,
+                        "scan_launches": kt["int8_scan"][1], "gemm_launches": launches}
+            key = f"batch{b}" if mode == 1 else f"mode0_batch{b}"
+            out[key] = {"qps": round(b * steps / elapsed, 1), "roofline": roof,
+                        "mode": "fixed budget 100, no proof" if mode == 1 else
+                                "adaptive budget with the lower-bound proof (exact)",
+                        "cpu_baseline": cpu.get(b)}
+            log(f"int8: mode {mode} batch {b}: {out[key]['qps']} queries/s")
     corpus.release()
     return out
 
@@ -346,7 +510,8 @@ def bench_ivf(args, ctx):
     di = hip.DeviceArray((B, k), np.uint32)
     stream = hip.Stream()
     out = {"workload": f"IVF-flat L2 top-{k}, {n}x{dim}, nlist {nlist}, batch {B}",
-           "kmeans_s": round(t_km, 3), "build_s": round(t_build, 3)}
+           "kmeans_s": round(t_km, 3), "build_s": round(t_build, 3),
+           "data_sha256": sha(db, q)}
     for nprobe in (4, 8, 32):
         gd, gi, gp = ivf.search(q, k, nprobe, want_probes=True)
         for i in (0, 1):
@@ -365,6 +530,21 @@ def bench_ivf(args, ctx):
             "candidates_per_query": round(cand_rows / B, 1),
             "roofline": roofline_hbm("ivf_scan<2>", f"ivf_{n}x{dim}_np{nprobe}_b{B}",
                                      cand_rows * (dim * 4 + 4 + 4), avg)}
+        if not args.no_cpu:
+            # IVFFlatSearch.search per query (scanProbedLists,
+            # IVFFlatSearch.swift:214-291) over the same lists, queries
+            # spread over the cores.
+            import concurrent.futures as cf
+
+            t0 = time.perf_counter()
+            with cf.ThreadPoolExecutor(CPU_THREADS) as ex:
+                list(ex.map(lambda i: part.search(q[i], k, nprobe), range(B)))
+            dt = time.perf_counter() - t0
+            out[f"nprobe{nprobe}"]["cpu_baseline"] = cpu_line(
+                B / dt, "queries/s", CPU_THREADS,
+                f"{B} queries through scanProbedLists restated (probes, exact dots.c-order "
+                f"scan of the probed lists, (distance, id) top-k), one query per thread, "
+                f"{dt:.2f} s")
         log(f"ivf: nprobe {nprobe}: {out[f'nprobe{nprobe}']['qps']} queries/s")
     ivf.release()
     corpus.release()
@@ -384,24 +564,47 @@ def bench_ivfpq(args, ctx):
     dim, nlist, m, nprobe, kadc, rer, B = 96, 8192, 48, 16, 100, 10, 1024
     log(f"ivfpq: {n} x 96 mixture, nlist {nlist}, M {m} x 8 bit, nprobe {nprobe}")
     db, q, _ = workloads.mixture_10m_96(nq=B, n=n)
-    corpus = ctx.upload(db)
+    data_sha = sha(db, q)
+    train = workloads.mixture_10m_96_train()
+    tc = ctx.upload(train)
     t = time.perf_counter()
-    coarse = corpus.kmeans(nlist, 2, M.METRIC_L2)
-    t_km = time.perf_counter() - t
-    rng = np.random.default_rng(5003)
-    books = np.ascontiguousarray(db[rng.choice(n, 256, replace=False)].reshape(256, m, 2)
-                                 .transpose(1, 0, 2)).astype(np.float32)
+    coarse, books = tc.ivfpq_train(nlist, m, args.pq_iters, M.METRIC_INNER_PRODUCT)
+    t_train = time.perf_counter() - t
+    tc.release()
+    corpus = ctx.upload(db)
     t = time.perf_counter()
     pq = corpus.ivfpq_build(coarse, books, M.METRIC_INNER_PRODUCT)
     t_build = time.perf_counter() - t
-    gs, gi = pq.search(q[:2], kadc, nprobe, rerank_k=rer)
+    gs, gi = pq.search(q[:4], kadc, nprobe, rerank_k=rer)
     codes, assign = pq.codes()
     offsets, ids = oracle.ivf_lists(assign, nlist)
-    for i in range(2):
+    for i in range(4):
         os_, oi = oracle.ivfpq_search(coarse, books, codes, offsets, ids, M.METRIC_INNER_PRODUCT, q[i], kadc,
                                       nprobe, rows=db, rerank_k=rer)
         if not (np.array_equal(gs[i], os_) and np.array_equal(gi[i], oi)):
             raise SystemExit("IVF-PQ parity gate failed")
+    # recall@10 of the reranked results against the exact inner-product top-10
+    nrec = 256
+    _, exact = corpus.flat_search(q[:nrec], rer, M.METRIC_INNER_PRODUCT)
+    _, got = pq.search(q[:nrec], kadc, nprobe, rerank_k=rer)
+    recall = float(np.mean([len(set(got[i]) & set(exact[i])) / rer for i in range(nrec)]))
+    cpu = {}
+    if not args.no_cpu:
+        import concurrent.futures as cf
+
+        ncpu = 1024
+        for rr in (0, rer):
+            t0 = time.perf_counter()
+            with cf.ThreadPoolExecutor(CPU_THREADS) as ex:
+                list(ex.map(lambda i: oracle.ivfpq_search(
+                    coarse, books, codes, offsets, ids, M.METRIC_INNER_PRODUCT, q[i], kadc, nprobe,
+                    rows=db if rr else None, rerank_k=rr), range(ncpu)))
+            dt = time.perf_counter() - t0
+            cpu[rr] = cpu_line(ncpu / dt, "queries/s", CPU_THREADS,
+                               f"{ncpu} queries through _IVFPQIndex.search restated (probes, "
+                               f"residual LUTs, sequential ADC, BoundedSortedList)"
+                               f"{' plus the exact rerank' if rr else ''}, one query per thread, "
+                               f"{dt:.2f} s")
     sizes = np.diff(offsets)
     probes = [oracle.ivfpq_probe(coarse, q[i], nprobe, M.METRIC_INNER_PRODUCT)[0] for i in range(B)]
     cand_per_query = float(np.mean([sizes[p].sum() for p in probes]))
@@ -412,8 +615,12 @@ def bench_ivfpq(args, ctx):
     stream = hip.Stream()
     out = {"workload": f"IVF-PQ ADC IP, {n}x{dim}, nlist {nlist}, M {m}, nprobe {nprobe}, "
                        f"top-{kadc} then exact rerank to {rer}, batch {B}",
-           "kmeans_s": round(t_km, 3), "build_s": round(t_build, 3),
-           "candidates_per_query": round(cand_per_query, 1)}
+           "training": f"mans_ivfpq_train on 262,144 mixture rows (seed 5003), {args.pq_iters} "
+                       f"iterations (coarse and per subspace), inner product",
+           "train_s": round(t_train, 3), "build_s": round(t_build, 3),
+           "candidates_per_query": round(cand_per_query, 1),
+           f"recall@{rer}_nprobe{nprobe}": round(recall, 4),
+           "data_sha256": data_sha}
     for rerank in (0, rer):
         def step(s, rerank=rerank):
             pq.search_device(dq.ptr, B, kadc, nprobe, rerank, dd.ptr, di.ptr, stream.handle)
@@ -423,7 +630,8 @@ def bench_ivfpq(args, ctx):
         key = "adc_rerank" if rerank else "adc"
         out[key] = {"qps": round(B * 5 / elapsed, 1),
                     "roofline": roofline_hbm("ivfpq_scan", f"ivfpq_{n}x{dim}_b{B}",
-                                             B * cand_per_query * (m + 4), avg)}
+                                             B * cand_per_query * (m + 4), avg),
+                    "cpu_baseline": cpu.get(rerank)}
         log(f"ivfpq: {key}: {out[key]['qps']} queries/s")
     pq.release()
     corpus.release()
@@ -438,6 +646,8 @@ def main():
     ap.add_argument("--batch", type=int, default=1024)
     ap.add_argument("--n", type=int, default=1_000_000)
     ap.add_argument("--pq-n", type=int, default=10_000_000)
+    ap.add_argument("--pq-iters", type=int, default=20,
+                    help="IVF-PQ training iterations (IVFPQConfiguration's default is 20)")
     ap.add_argument("--workload", default="flat", choices=["flat", "int8", "ivf", "ivfpq"])
     ap.add_argument("--quick", action="store_true", help="flat only, no 100k or per-config extras")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")

@@ -623,6 +623,57 @@ ORC_EXPORT int64_t orc_int8_search(const float *corpus, const float *norms, cons
     return result;
 }
 
+/* HostBatchWork.run over a batch without a GPU context
+ * (FlatGPUSearch.swift:754-779, 1003-1037): the queries fan out over
+ * `threads` workers; each query takes FlatGPUSearch.boundedExactSearch
+ * (FlatGPUSearch.swift:387-460: BoundedExactScan.search, mode 0, the
+ * adaptive proven-exact scan) when int8 planes are given and n >= 16384,
+ * and the fp32 host scan (hostSearch -> ParallelFlatScan with
+ * orc_slice_count(n, cores) slices, run by the worker itself) otherwise.
+ * Output stride = min(k, 256); route[i] (nullable): 1 int8, 0 fp32. */
+typedef struct {
+    const float *corpus, *norms, *queries;
+    const int8_t *codes;
+    const float *u, *w, *ns, *inv;
+    int64_t n, dim, k, cores, stride;
+    int metric;
+    float *out_dist;
+    uint32_t *out_ids;
+    int64_t *out_counts;
+    int32_t *route;
+} host_batch_ctx;
+
+static void host_batch_task(void *vctx, int64_t i) {
+    host_batch_ctx *c = (host_batch_ctx *)vctx;
+    const float *q = c->queries + i * c->dim;
+    float *od = c->out_dist + i * c->stride;
+    uint32_t *oi = c->out_ids + i * c->stride;
+    int64_t m = -1;
+    if (c->codes != NULL) {
+        int64_t budget = 0;
+        m = orc_int8_search(c->corpus, c->norms, c->codes, c->u, c->w, c->ns, c->inv, c->n, c->dim,
+                            q, c->k, c->metric, c->cores, 0, 0, 1, od, oi, &budget);
+    }
+    if (c->route) c->route[i] = m >= 0 ? 1 : 0;
+    if (m < 0)
+        m = orc_flat_search(c->corpus, c->norms, c->n, c->dim, q, c->k, c->metric, c->cores, 1, od,
+                            oi);
+    if (c->out_counts) c->out_counts[i] = m;
+}
+
+ORC_EXPORT void orc_host_batch_search(const float *corpus, const float *norms, const int8_t *codes,
+                                      const float *u_plane, const float *w_plane,
+                                      const float *normsq_plane, const float *invsqrt_plane,
+                                      int64_t n, int64_t dim, const float *queries, int64_t nq,
+                                      int64_t k, int metric, int64_t cores, int threads,
+                                      float *out_dist, uint32_t *out_ids, int64_t *out_counts,
+                                      int32_t *route) {
+    host_batch_ctx c = {corpus, norms, queries, codes, u_plane, w_plane, normsq_plane,
+                        invsqrt_plane, n, dim, k, cores, k < 256 ? k : 256, metric, out_dist,
+                        out_ids, out_counts, route};
+    parallel_for(nq, threads, host_batch_task, &c);
+}
+
 /* ------------------------------------------------------------------------ */
 /* IVF-flat (IVFFlatSearch.swift)                                            */
 /* ------------------------------------------------------------------------ */

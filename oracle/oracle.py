@@ -47,6 +47,9 @@ def lib() -> C.CDLL:
         L.orc_int8_search.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64,
                                       _i32, _i64, _i32, _i64, _i32, _vp, _vp, _vp]
         L.orc_int8_search.restype = _i64
+        L.orc_host_batch_search.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp,
+                                            _i64, _i64, _i32, _i64, _i32, _vp, _vp, _vp, _vp]
+        L.orc_host_batch_search.restype = None
         L.orc_ivf_assign.argtypes = [_vp, _vp, _i64, _i64, _vp, _vp, _i64, _i32, _vp]
         L.orc_ivf_lists.argtypes = [_vp, _i64, _i64, _vp, _vp]
         L.orc_ivf_probe.argtypes = [_vp, _vp, _i64, _i64, _vp, _i64, _i32, _vp]
@@ -185,6 +188,27 @@ def int8_search(corpus, norms, planes, q, k, metric, cores=None, mode=0, budget=
     if m < 0:
         return None
     return dist[:m], ids[:m], fb.value
+
+
+def host_batch_search(corpus, norms, planes, queries, k, metric, cores=None, threads=None):
+    """HostBatchWork.run over a batch: int8 bounded scan per query when
+    planes are given and n >= 16384, else the fp32 host scan.  Returns
+    (dist, ids, counts, route) with route 1 for the int8 scan."""
+    corpus, queries = _c(corpus, np.float32), _c(queries, np.float32)
+    norms = _c(norms, np.float32) if norms is not None else None
+    codes, u, w, ns, inv = planes if planes is not None else (None,) * 5
+    cores = cores or os.cpu_count() or 1
+    threads = threads or os.cpu_count() or 1
+    nq = queries.shape[0]
+    kk = min(k, 256)
+    dist = np.full((nq, kk), np.finfo(np.float32).max, np.float32)
+    ids = np.full((nq, kk), 0xFFFFFFFF, np.uint32)
+    counts = np.empty(nq, np.int64)
+    route = np.empty(nq, np.int32)
+    lib().orc_host_batch_search(_p(corpus), _p(norms), _p(codes), _p(u), _p(w), _p(ns), _p(inv),
+                                corpus.shape[0], corpus.shape[1], _p(queries), nq, k, metric,
+                                cores, threads, _p(dist), _p(ids), _p(counts), _p(route))
+    return dist, ids, counts, route
 
 
 def ivf_assign(rows, centroids, metric):

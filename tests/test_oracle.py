@@ -537,3 +537,21 @@ def test_int8_fixed_budget_over_every_row_is_the_exact_result(metric):
                                        budget=n)
         fd, fi = oracle.flat_search(corpus, norms, q, 10, metric, cores=8)
         assert np.array_equal(d, fd) and ids.tolist() == fi.tolist()
+
+
+def test_host_batch_route_takes_the_int8_scan_from_16384_rows():
+    # HostBatchWork.run (FlatGPUSearch.swift:1024-1036): boundedExactSearch
+    # for n >= 16384, the fp32 host scan below; both are exact, so the
+    # distances equal the fp32 scan's either way.
+    for n, want_route in ((16384, 1), (16383, 0)):
+        corpus = workloads.lcg_vectors(1, n, 32, seed=77)
+        planes = oracle.int8_build(corpus)
+        norms = oracle.row_norms(corpus)
+        q = workloads.lcg_vectors(1, 6, 32, seed=78)
+        d, ids, counts, route = oracle.host_batch_search(corpus, norms, planes, q, 10, COS, cores=8,
+                                                         threads=4)
+        assert np.all(route == want_route)
+        fd, fi, fc = oracle.flat_search_batch(corpus, norms, q, 10, COS, cores=8, threads=4)
+        assert np.array_equal(counts, fc) and np.array_equal(d, fd)
+        for i in range(q.shape[0]):
+            assert set(ids[i].tolist()) == set(fi[i].tolist())
