@@ -742,10 +742,10 @@ hipError_t stage_from_device(Slot* s, void* dst0, const void* src0, size_t b0, v
 // Runs the flat scan for queries already in device memory.  The proof loop
 // (kc x4 per round, exact keys past kc = 1024) mirrors the budget growth of
 // BoundedExactScan.swift:96-121.
-// MANS_BF3=0 keeps batches on the fp32 contraction.
-static bool bf3_enabled() {
+// MANS_BF16_SPLIT=0 keeps batches on the fp32 contraction.
+static bool bf16_split_enabled() {
     static const bool on = [] {
-        const char* e = std::getenv("MANS_BF3");
+        const char* e = std::getenv("MANS_BF16_SPLIT");
         return !(e && e[0] == '0');
     }();
     return on;
@@ -761,12 +761,13 @@ static int bf16_split_ensure(mans_ctx* ctx, const mans_corpus* cc, hipStream_t s
         c->bf_ok = false;
         return MANS_OK;
     }
-    hipError_t e = c->bf_split.ensure((size_t)c->n * c->dim * sizeof(uint32_t), ctx->fail_alloc);
+    hipError_t e = c->bf_hi.ensure((size_t)c->n * c->dim * sizeof(uint16_t), ctx->fail_alloc);
+    if (e == hipSuccess) e = c->bf_rec.ensure((size_t)c->n * 4 * sizeof(float), ctx->fail_alloc);
     if (e == hipSuccess) e = c->bf_flag.ensure(sizeof(uint32_t), ctx->fail_alloc);
     if (e == hipSuccess) e = hipMemsetAsync(c->bf_flag.p, 0, sizeof(uint32_t), st);
     if (e == hipSuccess)
-        e = launch_split_bf16((const float*)c->rows.p, c->n, (int)c->dim, (uint32_t*)c->bf_split.p,
-                              (uint32_t*)c->bf_flag.p, false, st);
+        e = launch_split_rows((const float*)c->rows.p, (const float*)c->norms.p, c->n, (int)c->dim,
+                              (uint16_t*)c->bf_hi.p, (float*)c->bf_rec.p, (uint32_t*)c->bf_flag.p, st);
     uint32_t flag = 1;
     if (e == hipSuccess)
         e = hipMemcpyAsync(&flag, c->bf_flag.p, sizeof(uint32_t), hipMemcpyDeviceToHost, st);
@@ -829,15 +830,21 @@ static int flat_search_chunk(mans_ctx* ctx, const mans_corpus* c, const float* d
         if (pending.empty() && !exact && plan_gemm(n, dim, npend, kc, &gp)) {
             // First round of a batch: MFMA contraction + per-query merge,
             // on split-bf16 MFMA when the corpus allows it, else fp32 MFMA.
-            const bool bf3 = bf3_enabled() && bf16_split_ensure(ctx, c, st) == MANS_OK && c->bf_ok;
-            if (bf3) gp.lps = 4;
+            // The split path's keys are looser (the rows keep only their
+            // high parts): it keeps kGemmMaxKc candidates.
+            const bool bf = bf16_split_enabled() && bf16_split_ensure(ctx, c, st) == MANS_OK && c->bf_ok;
+            if (bf && kc < kGemmMaxKc) {
+                kc = kGemmMaxKc;
+                (void)plan_gemm(n, dim, npend, kc, &gp);
+            }
+            if (bf) gp.lps = 4;
             const size_t lbytes = gemm_lists_bytes(gp, npend);
             e = slot->cand.ensure(lbytes + (size_t)npend * sizeof(uint64_t), ctx->fail_alloc);
             if (e == hipSuccess) e = slot->status.ensure((size_t)npend, ctx->fail_alloc);
             if (e == hipSuccess) e = slot->status_h.ensure((size_t)npend);
-            if (e == hipSuccess && bf3)
+            if (e == hipSuccess && bf)
                 e = slot->qsplit.ensure((size_t)npend * dim * sizeof(uint32_t), ctx->fail_alloc);
-            if (e == hipSuccess && bf3)
+            if (e == hipSuccess && bf)
                 e = slot->qbad.ensure((size_t)npend * sizeof(uint32_t), ctx->fail_alloc);
             if (e != hipSuccess) return hip_fail(e, "flat scan workspace");
             FlatBuffers fb;
@@ -847,26 +854,29 @@ static int flat_search_chunk(mans_ctx* ctx, const mans_corpus* c, const float* d
             // after the round's one synchronisation, no copy).
             fb.status = (uint8_t*)slot->status_h.p;
             uint64_t* lists = (uint64_t*)slot->cand.p;
-            uint64_t* qbound = bf3 ? lists + lbytes / sizeof(uint64_t) : nullptr;
-            const uint32_t* qbad = bf3 ? (const uint32_t*)slot->qbad.p : nullptr;
+            uint64_t* qbound = bf ? lists + lbytes / sizeof(uint64_t) : nullptr;
+            const uint32_t* qbad = bf ? (const uint32_t*)slot->qbad.p : nullptr;
             const float* rows = (const float*)c->rows.p;
             const float* norms = (const float*)c->norms.p;
-            if (bf3) {
+            if (bf) {
                 uint32_t* qs = (uint32_t*)slot->qsplit.p;
-                const uint32_t* rs = (const uint32_t*)c->bf_split.p;
+                const uint16_t* hi = (const uint16_t*)c->bf_hi.p;
+                const float* rec = (const float*)c->bf_rec.p;
                 ctx->time_begin(slot, st);
                 e = hipMemsetAsync(slot->qbad.p, 0, (size_t)npend * sizeof(uint32_t), st);
                 if (e == hipSuccess)
-                    e = launch_split_bf16(d_q, npend, dim, qs, (uint32_t*)slot->qbad.p, true, st);
+                    e = launch_split_queries(d_q, npend, dim, qs, (uint32_t*)slot->qbad.p, st);
                 if (e == hipSuccess)
-                    e = launch_flat_bf3(gp, true, rs, norms, n, dim, qs, d_q, npend, (int)metric,
-                                        nullptr, lists, st);
-                if (e == hipSuccess) e = launch_bf3_bounds(gp, npend, lists, qbound, st);
+                    e = launch_flat_bf2(gp, true, hi, rec, norms, n, dim, qs, d_q, npend,
+                                        (int)metric, nullptr, lists, st);
+                if (e == hipSuccess)
+                    e = launch_bf2_bounds(gp, npend, keff, lists, rows, norms, dim, d_q,
+                                          (int)metric, qbound, st);
                 ctx->time_end(slot, st, "flat_bound");
                 ctx->time_begin(slot, st);
                 if (e == hipSuccess)
-                    e = launch_flat_bf3(gp, false, rs, norms, n, dim, qs, d_q, npend, (int)metric,
-                                        qbound, lists, st);
+                    e = launch_flat_bf2(gp, false, hi, rec, norms, n, dim, qs, d_q, npend,
+                                        (int)metric, qbound, lists, st);
                 ctx->time_end(slot, st, "flat_gemm");
             } else {
                 ctx->time_begin(slot, st);

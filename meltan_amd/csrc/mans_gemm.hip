@@ -254,26 +254,31 @@ __global__ __launch_bounds__(256) void flat_gemm_f32(
 // ---------------------------------------------------------------------------
 // Batched queries on bf16 MFMA with fp32-level accuracy (split products).
 //
-// Every value x in [2^-50, 2^50] (or 0) is split once into bf16 parts
+// Every query value x in [2^-50, 2^50] (or 0) is split into bf16 parts
 // x = xh + xl + r: xh = bf16(x), xl = bf16(x - xh) (x - xh is exact in
 // fp32), both rounded to nearest even, so |x - xh| <= 2^-8 |x| and
-// |r| <= 2^-16 |x|.  The contraction sums qh vh, qh vl and ql vh with
-// v_mfma_f32_32x32x16_bf16 into three fp32 accumulators (each product of
-// two bf16 values is exact in fp32), combined as hh + (hl + lh).  The
-// omitted terms ql vl + (qh + ql) rv + rq (vh + vl) + rq rv are at most
-// 3.01 2^-16 |q_i v_i| per element, the accumulations add at most
-// gamma_d (u = 2^-23) (1 + 2^-7 + 2^-7) sum |q_i v_i| and the two final
-// additions 2^-22 of it, so
-//   |f - q.v| <= g sum |q_i v_i|,  g = 1.024 gamma_d + 3.01 2^-16 + 2^-22,
-// and the keys are the fp32 path's lower bounds computed with a unit
-// roundoff u_eff for which gamma_d(u_eff) = g (>= every other error term
-// those bounds cover).  Values outside the range (huge, tiny, inf, NaN)
-// are flagged when split: a corpus with any such value keeps the fp32
-// contraction, and a flagged query is re-run by the streaming scan.
+// |r| <= 2^-16 |x|.  A row keeps only its high part vh = bf16(v) (same
+// rounding) and e_v >= ||v - vh||, the norm of its remainder (summed in
+// double, rounded up to fp32).  The contraction sums qh vh and ql vh with
+// v_mfma_f32_32x32x16_bf16 into two fp32 accumulators (each product of two
+// bf16 values is exact in fp32), added at the end.  Since
+//   q.v = (qh + ql) vh + r vh + q (v - vh),
+// the sum f satisfies
+//   |f - q.v| <= g sum |q_i v_i| + ||q|| e_v,
+//   g = 1.024 gamma_d (u = 2^-23) + 1.01 2^-16 + 2^-22
+// (the accumulations over (1 + 2^-8)^3 sum |q_i v_i|, |r vh| and the final
+// additions; the last term by Cauchy-Schwarz).  The keys are the fp32
+// path's lower bounds computed with a unit roundoff u_eff for which
+// gamma_d(u_eff) = g (>= every other error term those bounds cover), minus
+// the row's remainder term: ||q|| e_v for inner product, 2 ||q|| e_v for
+// L2 and e_v / ||v|| for cosine, each times 1 + 2^-12 (which covers the
+// roundings of the norms and of the key arithmetic).  Values outside the
+// range (huge, tiny, inf, NaN) are flagged when split: a corpus with any
+// such value keeps the fp32 contraction, and a flagged query is re-run by
+// the streaming scan.
 //
-// The split parts are stored per 8 elements as [8 hi | 8 lo] (32 bytes),
-// so a row keeps its fp32 size and one 16-element MFMA step of a lane is
-// two 16-byte reads.
+// Queries are stored per 8 elements as [8 hi | 8 lo] (32 bytes); rows as
+// their dim bf16 high parts (half the fp32 size) plus e_v.
 //
 // The epilogue admits a key only when it is at or below the lane's
 // threshold (its largest slot, or the query's bound): a first launch over
@@ -292,11 +297,10 @@ __device__ __forceinline__ bool split_in_range(float x) {
     return a == 0.0f || (a >= 0x1p-50f && a <= 0x1p50f);
 }
 
-// One thread per 8 elements of `count` rows of dim (multiple of 8) floats;
-// bad[row] (per_row) or bad[0] gets 1 for a value outside the range.
-__global__ void split_bf16_kernel(const float* __restrict__ src, int64_t count, int dim,
-                                  uint32_t* __restrict__ dst, uint32_t* __restrict__ bad,
-                                  int per_row) {
+// One thread per 8 elements of `count` queries of dim (multiple of 8)
+// floats; bad[query] gets 1 for a value outside the range.
+__global__ void split_queries_kernel(const float* __restrict__ src, int64_t count, int dim,
+                                     uint32_t* __restrict__ dst, uint32_t* __restrict__ bad) {
     const int cpr = dim >> 3;
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= count * cpr) return;
@@ -320,15 +324,79 @@ __global__ void split_bf16_kernel(const float* __restrict__ src, int64_t count, 
     uint32_t* d = dst + row * dim + 8 * c;
     *reinterpret_cast<i4v*>(d) = i4v{(int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
     *reinterpret_cast<i4v*>(d + 4) = i4v{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3]};
-    if (!ok) atomicOr(bad + (per_row ? row : 0), 1u);
+    if (!ok) atomicOr(bad + row, 1u);
 }
 
-hipError_t launch_split_bf16(const float* src, int64_t count, int dim, uint32_t* dst,
-                             uint32_t* bad, bool per_row, hipStream_t s) {
+hipError_t launch_split_queries(const float* src, int64_t count, int dim, uint32_t* dst,
+                                uint32_t* bad, hipStream_t s) {
     const int64_t threads = count * (dim / 8);
     if (threads <= 0) return hipSuccess;
-    hipLaunchKernelGGL(split_bf16_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
-                       src, count, dim, dst, bad, per_row ? 1 : 0);
+    hipLaunchKernelGGL(split_queries_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                       s, src, count, dim, dst, bad);
+    return hipGetLastError();
+}
+
+// One wave per row of `count` rows of dim (multiple of 8) floats: hi gets
+// the row's bf16 high parts and recs four planes of `count` floats:
+// 1 / sqrt(vn) and e' / sqrt(vn) (cosine), sqrt(vn) and e' (L2, inner
+// product), with vn the row's squared norm and e' >= (1 + 2^-12) ||v - vh||
+// (summed in double, rounded up); bad[0] gets 1 for a value outside the
+// range.
+__global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict__ src,
+                                                         const float* __restrict__ norms,
+                                                         int64_t count, int dim,
+                                                         uint16_t* __restrict__ hi,
+                                                         float* __restrict__ recs,
+                                                         uint32_t* __restrict__ bad) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= count) return;
+    const float* s = src + row * dim;
+    double acc = 0.0;
+    bool ok = true;
+    for (int c = lane; c < dim / 8; c += 64) {
+        const f4v a = *reinterpret_cast<const f4v*>(s + 8 * c);
+        const f4v b = *reinterpret_cast<const f4v*>(s + 8 * c + 4);
+        const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        uint32_t h[4];
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+            const uint32_t h0 = bf16_rne_bits(x[i]), h1 = bf16_rne_bits(x[i + 1]);
+            // The remainders are exact in fp32, their squares in double.
+            const double r0 = (double)(x[i] - __uint_as_float(h0 << 16));
+            const double r1 = (double)(x[i + 1] - __uint_as_float(h1 << 16));
+            acc += r0 * r0;
+            acc += r1 * r1;
+            h[i / 2] = h0 | (h1 << 16);
+            ok = ok && split_in_range(x[i]) && split_in_range(x[i + 1]);
+        }
+        *reinterpret_cast<i4v*>(hi + row * dim + 8 * c) = i4v{(int)h[0], (int)h[1], (int)h[2], (int)h[3]};
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
+    if (lane == 0) {
+        // The double sum and square root are off by far less than 2^-40;
+        // the factor 1 + 2^-12 covers the roundings of the norms and of the
+        // key arithmetic that use e'.
+        const double e = sqrt(acc) * (1.0 + 0x1p-40) * (1.0 + 0x1p-12);
+        float f = (float)e;
+        if ((double)f < e) f = __uint_as_float(__float_as_uint(f) + 1u);
+        const float vn = norms[row];
+        const float ws = sqrtf(vn);
+        const float wr = vn > 0.0f ? 1.0f / ws : 0.0f;
+        recs[row] = wr;
+        recs[count + row] = f * wr;
+        recs[2 * count + row] = ws;
+        recs[3 * count + row] = f;
+    }
+    if (!ok) atomicOr(bad, 1u);
+}
+
+hipError_t launch_split_rows(const float* src, const float* norms, int64_t count, int dim,
+                             uint16_t* hi, float* recs, uint32_t* bad, hipStream_t s) {
+    if (count <= 0) return hipSuccess;
+    hipLaunchKernelGGL(split_rows_kernel, dim3((unsigned)((count + 3) / 4)), dim3(256), 0, s, src,
+                       norms, count, dim, hi, recs, bad);
     return hipGetLastError();
 }
 
@@ -338,76 +406,91 @@ typedef __bf16 bf8v __attribute__((ext_vector_type(8)));
 // rows: wave w takes query group w & 3 (32 queries) and half w >> 2 of the
 // k range, so a wave keeps only its half of the query's split parts in
 // registers and two waves fit on a SIMD (one hides the other's latencies).
-// Per 32-row tile the two halves' sums (hh + (hl + lh) over each half) are
-// exchanged through LDS and added (the same IEEE sum in either wave), and
-// each wave keys 8 of the 16 rows a lane holds, keeping its own lane lists
-// (4 lists per query and segment: half x lane half).
+// Per 32-row tile the two halves' sums are exchanged through LDS and added
+// (the same IEEE sum in either wave), and each wave keys 8 of the 16 rows a
+// lane holds, keeping its own lane lists (4 lists per query and segment:
+// half x lane half).
 //
 // Tiles reach LDS by direct global-to-LDS loads (global_load_lds, 16 bytes
-// per lane) into a ring of two tile slots: tile t + 1 loads while tile t is
-// contracted, without holding registers.  A slot holds, per k half, 32 rows
-// x CPR 16-byte chunks unpadded; chunk c of row r sits at c ^ (r & SWZ), so
-// the 32 lanes of a half-wave reading one chunk of 32 rows hit distinct
-// banks.
-constexpr int kBf3Waves = 8;
-constexpr int kBf3Slots = 2;
-constexpr int kBf3Lists = 4;  // lane lists per query and segment
+// per lane) into a ring of three slots, two tiles ahead, without holding
+// registers.  A slot holds, per k half, 32 rows x CPR 16-byte chunks
+// unpadded; chunk c of row r sits at c ^ (r & SWZ), so the lanes of a
+// half-wave reading one chunk of 32 rows spread over the banks.  Each wave
+// issues the same number of row loads per tile (a tile that does not split
+// evenly over the block's lanes is padded) and wave 0 one more, the tile's
+// row records, into a ring of four record slots; so a wave waits for tile t
+// while tile t + 1's loads stay in flight.
+//
+// Per iteration t a wave computes the keys of tile t - 1 (branch-free, in
+// the same block as tile t's MFMAs so the scheduler can place them between
+// them), then tile t's MFMAs, then the insertion path for tile t - 1's keys
+// at or below the lane's threshold, then sends tile t's partner half.
+constexpr int kBf2Waves = 8;
+constexpr int kBf2Slots = 3;
+constexpr int kBf2RecSlots = 4;
+constexpr int kBf2Lists = 4;  // lane lists per query and segment
 
 template <int DIM>
-struct Bf3Shape {
+struct Bf2Shape {
     static constexpr int NS = DIM / 16;  // MFMA k-steps per row
     static constexpr int NH = NS / 2;    // k-steps per half
-    static constexpr int CPR = 4 * NH;   // 16-byte chunks of a row per half
+    static constexpr int CPR = 2 * NH;   // 16-byte chunks of a row per half
     static constexpr int LOWBIT = CPR & -CPR;
     static constexpr int SWZ = (LOWBIT < 16 ? LOWBIT : 16) - 1;
     static constexpr int HALF_CHUNKS = kGemmRows * CPR;
     static constexpr int TILE_CHUNKS = 2 * HALF_CHUNKS;
-    static constexpr int TILE_BYTES = 16 * TILE_CHUNKS;
-    static constexpr int WAVE_INSTS = (TILE_CHUNKS + 64 * kBf3Waves - 1) / (64 * kBf3Waves);
+    static constexpr int LOADS = (TILE_CHUNKS + 64 * kBf2Waves - 1) / (64 * kBf2Waves);
+    static constexpr int SLOT_BYTES = 16 * 64 * kBf2Waves * LOADS;
     static_assert(DIM % 32 == 0, "unsupported dimension");
 };
 
 template <int DIM>
-size_t bf3_lds_bytes() {
-    return kBf3Slots * (size_t)Bf3Shape<DIM>::TILE_BYTES +
-           sizeof(float) * (2 * kBf3Waves * 64 * 8 + kBf3Slots * kGemmRows + 4 * kGemmRows);
+size_t bf2_lds_bytes() {
+    return kBf2Slots * (size_t)Bf2Shape<DIM>::SLOT_BYTES +
+           sizeof(float) * (kBf2RecSlots * 3 * kGemmRows + 2 * kBf2Waves * 64 * 8);
 }
 
-struct Bf3Args {
+struct Bf2Args {
     int nseg;
     int nqb;
     int64_t rows_per_seg;     // multiple of kGemmRows
     int64_t seg_rows;         // rows scanned from each segment's start
     float abs_slack;
     const uint64_t* qbound;   // per query (BOUNDED)
-    uint64_t* lists;          // [nq][nseg][kBf3Lists][C]
+    uint64_t* lists;          // [nq][nseg][kBf2Lists][C]
 };
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
+// s_waitcnt vmcnt(N) through the builtin, so the compiler's own wait
+// insertion knows which loads are complete (expcnt and lgkmcnt at their
+// no-wait values).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt out of range");
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// grid: nseg * nqb blocks (1-D, XCD mapping as flat_gemm_f32); block 512.
-// split_rows / split_q: the split parts of the rows and of the queries.
-template <int DIM, int METRIC, int C, bool BOUNDED>
-__global__ __launch_bounds__(512, 1) void flat_gemm_bf16x3(
-    const uint32_t* __restrict__ split_rows, const float* __restrict__ norms, int64_t n,
-    const uint32_t* __restrict__ split_q, const float* __restrict__ queries, int64_t nq,
-    BoundCoef bc, Bf3Args ga) {
-    using G = Bf3Shape<DIM>;
+// One wave's work over the block's segment; KP: the wave's k half.
+template <int DIM, int METRIC, int C, bool BOUNDED, int KP>
+__device__ __forceinline__ void bf2_segment(const uint16_t* __restrict__ hi_rows,
+                                            const float* __restrict__ wplane,
+                                            const float* __restrict__ cplane,
+                                            const float* __restrict__ norms, int64_t n,
+                                            const uint32_t* __restrict__ split_q,
+                                            const float* __restrict__ queries, int64_t nq,
+                                            const BoundCoef& bc, const Bf2Args& ga, int wave) {
+    using G = Bf2Shape<DIM>;
     constexpr int NH = G::NH, CPR = G::CPR, SWZ = G::SWZ;
     extern __shared__ uint64_t lds[];
-    uint8_t* ring = reinterpret_cast<uint8_t*>(lds);                      // [slot][half][32][CPR][16]
-    float* xch = reinterpret_cast<float*>(ring + kBf3Slots * G::TILE_BYTES);  // [2][wave][64][8]
-    float* tvn = xch + 2 * kBf3Waves * 64 * 8;  // [slot][32] raw vn
-    float* tva = tvn + kBf3Slots * kGemmRows;  // [2][32] vn (NaN past the segment)
-    float* tvb = tva + 2 * kGemmRows;          // [2][32] sqrt(vn), or 1 / sqrt(vn) for cosine
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int qg = wave & 3, kp = wave >> 2;
+    uint8_t* ring = reinterpret_cast<uint8_t*>(lds);  // [slot][half][32][CPR][16]
+    // Per record slot: w[32], c[32], vn[32].
+    float* trec = reinterpret_cast<float*>(ring + kBf2Slots * G::SLOT_BYTES);
+    // Partner sums: [2][wave][64] f4v, first and second four.
+    f4v* xa = reinterpret_cast<f4v*>(trec + kBf2RecSlots * 3 * kGemmRows);
+    f4v* xb = xa + 2 * kBf2Waves * 64;
+    const int lane = threadIdx.x & 63;
+    const int qg = wave & 3;
     const int h = lane >> 5, col = lane & 31;
 
     const int b = blockIdx.x, grp = 8 * ga.nqb;
@@ -420,7 +503,7 @@ __global__ __launch_bounds__(512, 1) void flat_gemm_bf16x3(
     bf8v qh[NH], ql[NH];
 #pragma unroll
     for (int s = 0; s < NH; ++s) {
-        const uint32_t* p = split_q + qrow * DIM + 8 * (2 * (kp * NH + s) + h);
+        const uint32_t* p = split_q + qrow * DIM + 8 * (2 * (KP * NH + s) + h);
         qh[s] = __builtin_bit_cast(bf8v, *reinterpret_cast<const i4v*>(p));
         ql[s] = __builtin_bit_cast(bf8v, *reinterpret_cast<const i4v*>(p + 4));
     }
@@ -453,100 +536,110 @@ __global__ __launch_bounds__(512, 1) void flat_gemm_bf16x3(
 
     const int64_t seg0 = (int64_t)seg * ga.rows_per_seg;
     const int64_t seg1 = seg0 + ga.seg_rows < n ? seg0 + ga.seg_rows : n;
-    const int64_t ntiles = seg1 > seg0 ? (seg1 - seg0 + kGemmRows - 1) / kGemmRows : 0;
+    const int ntiles = seg1 > seg0 ? (int)((seg1 - seg0 + kGemmRows - 1) / kGemmRows) : 0;
 
-    // Loads tile t into slot t % 2 (both k halves), and its row norms.  Rows
-    // past the segment's end load its last row.
-    auto issue = [&](int64_t t) {
-        if (t >= ntiles) return;
-        uint8_t* base = ring + (int)(t % kBf3Slots) * G::TILE_BYTES;
+    // Per-lane byte offsets of this lane's chunks within a tile (row r of
+    // the tile), the same for every tile; padding positions past the tile
+    // load the tile's first chunk.
+    uint32_t voff[G::LOADS];
+    int vrow[G::LOADS];
 #pragma unroll
-        for (int u = 0; u < G::WAVE_INSTS; ++u) {
-            const int inst = wave * G::WAVE_INSTS + u;
-            const int p = inst * 64 + lane;
-            if (G::TILE_CHUNKS % (64 * kBf3Waves) == 0 || p < G::TILE_CHUNKS) {
-                const int half = p / G::HALF_CHUNKS, rem = p - half * G::HALF_CHUNKS;
-                const int r = rem / CPR, qq = rem - r * CPR;
-                const int c = qq ^ (r & SWZ);
-                int64_t row = seg0 + t * kGemmRows + r;
-                row = row < seg1 ? row : seg1 - 1;
-                const uint8_t* src = reinterpret_cast<const uint8_t*>(split_rows + row * DIM) +
-                                     half * (16 * CPR) + 16 * c;
-                __builtin_amdgcn_global_load_lds(src, (lds_ptr_t)(base + inst * 1024), 16, 0, 0);
+    for (int u = 0; u < G::LOADS; ++u) {
+        int p = (wave * G::LOADS + u) * 64 + lane;
+        p = p < G::TILE_CHUNKS ? p : 0;
+        const int half = p / G::HALF_CHUNKS, rem = p - half * G::HALF_CHUNKS;
+        const int r = rem / CPR, qq = rem - r * CPR;
+        const int c = qq ^ (r & SWZ);
+        vrow[u] = r;
+        voff[u] = (uint32_t)(r * DIM * 2 + half * (16 * CPR) + 16 * c);
+    }
+    const uint8_t* seg_base = reinterpret_cast<const uint8_t*>(hi_rows + seg0 * DIM);
+    // Waves 0, 1 and 2 load a tile's w, c and vn planes.
+    const float* plane = wave == 0 ? wplane : (wave == 1 ? cplane : norms);
+    // The query parts and the bound are in registers before the first tile
+    // loads are issued.
+    wait_vmcnt<0>();
+
+    // Loads tile t into ring slot `slot` (both k halves) and its record
+    // planes into record slot t % 4.  Rows past the segment's end load its
+    // last row.
+    auto issue = [&](int t, int slot) {
+        if (t >= ntiles) return;
+        const int64_t left = seg1 - (seg0 + (int64_t)t * kGemmRows);
+        const uint8_t* tb = seg_base + (int64_t)t * (kGemmRows * DIM * 2);
+        uint8_t* dst = ring + slot * G::SLOT_BYTES + wave * G::LOADS * 1024;
+        if (left >= kGemmRows) {
+#pragma unroll
+            for (int u = 0; u < G::LOADS; ++u)
+                __builtin_amdgcn_global_load_lds(tb + voff[u], (lds_ptr_t)(dst + u * 1024), 16, 0, 0);
+        } else {
+#pragma unroll
+            for (int u = 0; u < G::LOADS; ++u) {
+                const int back = vrow[u] < left ? 0 : vrow[u] - (int)left + 1;
+                __builtin_amdgcn_global_load_lds(tb + voff[u] - back * (DIM * 2),
+                                                 (lds_ptr_t)(dst + u * 1024), 16, 0, 0);
             }
         }
-        if (wave == 0 && lane < kGemmRows) {
-            int64_t row = seg0 + t * kGemmRows + lane;
+        if (wave < 3) {
+            int64_t row = seg0 + (int64_t)t * kGemmRows + (lane & 31);
             row = row < seg1 ? row : seg1 - 1;
-            __builtin_amdgcn_global_load_lds(norms + row,
-                                             (lds_ptr_t)(tvn + (int)(t % kBf3Slots) * kGemmRows),
-                                             4, 0, 0);
+            if (lane < kGemmRows)
+                __builtin_amdgcn_global_load_lds(
+                    plane + row, (lds_ptr_t)(trec + ((t & (kBf2RecSlots - 1)) * 3 + wave) * kGemmRows),
+                    4, 0, 0);
         }
     };
 
-    // Tile t's sums: the partner half's 8 (rows it keys) go to LDS buffer
-    // t & 1, this wave's 8 stay in `keep`.  After the next barrier the
-    // partner's 8 for this wave are read back, added (the same IEEE sum in
-    // either wave) and keyed: rows 8 (v / 4) + 4 h + v % 4 for
-    // v = 8 KP .. 8 KP + 7, branch-free, then the insertion path only for a
-    // lane with a key at or below its threshold.
-    auto send = [&](const f16v& part, int64_t t, float (&keep)[8], auto kpc) {
-        constexpr int KP = decltype(kpc)::value;
-        constexpr int other = 8 * (1 - KP), my0 = 8 * KP;
-        float* mine = xch + (((int)(t & 1) * kBf3Waves + wave) * 64 + lane) * 8;
-        *reinterpret_cast<f4v*>(mine) = f4v{part[other], part[other + 1], part[other + 2], part[other + 3]};
-        *reinterpret_cast<f4v*>(mine + 4) =
-            f4v{part[other + 4], part[other + 5], part[other + 6], part[other + 7]};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) keep[i] = part[my0 + i];
-    };
-    auto receive_and_offer = [&](const float (&keep)[8], int64_t t, auto kpc) {
-        constexpr int KP = decltype(kpc)::value;
-        constexpr int my0 = 8 * KP;
-        const float* theirs = xch + (((int)(t & 1) * kBf3Waves + ((wave + 4) & 7)) * 64 + lane) * 8;
-        const f4v r0 = *reinterpret_cast<const f4v*>(theirs);
-        const f4v r1 = *reinterpret_cast<const f4v*>(theirs + 4);
-        float f[8];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            f[i] = keep[i] + r0[i];
-            f[4 + i] = keep[4 + i] + r1[i];
-        }
-        const int tb = (int)(t & 1) * kGemmRows;
-        float key[8];
+    // Keys of tile t's 8 rows of this lane (rows 8 (v / 4) + 4 h + v % 4
+    // for v = 8 KP .. 8 KP + 7): this wave's sums plus the partner's, read
+    // from LDS buffer t & 1.
+    auto keys = [&](const float (&keep)[8], int t, float (&key)[8]) {
+        const int xo = ((t & 1) * kBf2Waves + ((wave + 4) & 7)) * 64 + lane;
+        const f4v r0 = xa[xo];
+        const f4v r1 = xb[xo];
+        const float* tr = trec + (t & (kBf2RecSlots - 1)) * 3 * kGemmRows;
 #pragma unroll
         for (int g = 0; g < 2; ++g) {
-            const int m0 = 8 * ((my0 >> 2) + g) + 4 * h;
-            const f4v vna = *reinterpret_cast<const f4v*>(tva + tb + m0);
-            const f4v wva = *reinterpret_cast<const f4v*>(tvb + tb + m0);
+            const int m0 = 8 * (2 * KP + g) + 4 * h;
+            const f4v w4 = *reinterpret_cast<const f4v*>(tr + m0);
+            const f4v c4 = *reinterpret_cast<const f4v*>(tr + kGemmRows + m0);
+            f4v v4 = {};
+            if (METRIC != kMetricIP) v4 = *reinterpret_cast<const f4v*>(tr + 2 * kGemmRows + m0);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const float fv = f[4 * g + j], vn = vna[j], wv = wva[j];
+                const int i = 4 * g + j;
+                const float fv = keep[i] + (g == 0 ? r0[j] : r1[j]);
+                const float wv = w4[j], vc = c4[j], vn = v4[j];
                 float k;
                 if (METRIC == kMetricIP) {
-                    k = (-fv - (sq * wv) * bc.c_ip) - ga.abs_slack;
+                    k = (-fv - sq * (wv * bc.c_ip + vc)) - ga.abs_slack;
                 } else if (METRIC == kMetricL2) {
                     float dd = qn - 2.0f * fv + vn;
                     dd = dd > 0.0f ? dd : 0.0f;
-                    k = (dd - (qn + vn + 2.0f * (sq * wv)) * bc.c_l2) - ga.abs_slack;
+                    k = (dd - ((qn + vn + 2.0f * (sq * wv)) * bc.c_l2 + sq * (2.0f * vc))) -
+                        ga.abs_slack;
                 } else {
-                    // A zero row has wv = 0 and key 1 - eps (both paths give
-                    // exactly 1); past the segment vn and wv are NaN.
-                    k = (1.0f - fv * (rq * wv)) - eps_all;
+                    // A zero row has wv = vc = 0 and key 1 - eps (both paths
+                    // give exactly 1).
+                    k = (1.0f - fv * (rq * wv)) - (eps_all + vc);
                     k = vn < vn_tiny ? -1.0f : k;
                 }
-                key[4 * g + j] = k;
+                key[i] = k;
             }
         }
+    };
+    // The insertion path, only for a lane with a key at or below its
+    // threshold.
+    auto offer = [&](const float (&key)[8], int t) {
         float mn = key[0];
 #pragma unroll
         for (int i = 1; i < 8; ++i) mn = fminf(mn, key[i]);
         if (mn <= thr) {
-            const int64_t base = seg0 + t * kGemmRows;
+            const int64_t base = seg0 + (int64_t)t * kGemmRows;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 if (key[i] <= thr) {
-                    const int v = my0 + i;
+                    const int v = 8 * KP + i;
                     const int m = 8 * (v >> 2) + 4 * h + (v & 3);
                     const uint64_t slot = pack_slot(key[i], (uint32_t)(base + m));
                     if (slot <= bound) {
@@ -558,75 +651,158 @@ __global__ __launch_bounds__(512, 1) void flat_gemm_bf16x3(
             }
         }
     };
+    // Tile t's sums: the partner half's 8 (rows it keys) go to LDS buffer
+    // t & 1, this wave's 8 stay in `keep`.
+    auto send = [&](const f16v& part, int t, float (&keep)[8]) {
+        constexpr int other = 8 * (1 - KP), my0 = 8 * KP;
+        const int xo = ((t & 1) * kBf2Waves + wave) * 64 + lane;
+        xa[xo] = f4v{part[other], part[other + 1], part[other + 2], part[other + 3]};
+        xb[xo] = f4v{part[other + 4], part[other + 5], part[other + 6], part[other + 7]};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) keep[i] = part[my0 + i];
+    };
 
-    issue(0);
+    issue(0, 0);
+    issue(1, 1);
     float keep[8] = {};
-    for (int64_t t = 0; t < ntiles; ++t) {
-        // Tile t is in LDS once this wave's loads are done; the barrier
-        // publishes every wave's part (and the previous tile's sums and
-        // norms) and frees the other slot (tile t - 1).
-        wait_vmcnt<0>();
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    int cslot = 0, islot = 2;  // t % 3 and (t + 2) % 3
+    for (int t = 0; t < ntiles; ++t) {
+        // Tile t is in LDS once this wave's loads of it are done (those of
+        // tile t + 1 may still be in flight); the barrier publishes every
+        // wave's loads and parts and frees slot (t - 1) % 3 for tile t + 2.
+        if (t + 1 < ntiles) {
+            if (wave < 3) wait_vmcnt<G::LOADS + 1>();
+            else wait_vmcnt<G::LOADS>();
+        } else {
+            wait_vmcnt<0>();
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        issue(t + 1);
-        if (wave == 0 && lane < kGemmRows) {
-            const int64_t row = seg0 + t * kGemmRows + lane;
-            const float vn = tvn[(int)(t % kBf3Slots) * kGemmRows + lane];
-            const bool in = row < seg1;
-            const float nan = __int_as_float(0x7FC00000);
-            const int at = (int)(t & 1) * kGemmRows + lane;
-            tva[at] = in ? vn : nan;
-            tvb[at] = !in ? nan
-                          : (METRIC == kMetricCosine ? (vn > 0.0f ? 1.0f / sqrtf(vn) : 0.0f)
-                                                     : sqrtf(vn));
-        }
-        const uint8_t* xl = ring + (int)(t % kBf3Slots) * G::TILE_BYTES +
-                            kp * (16 * G::HALF_CHUNKS) + col * CPR * 16;
+        issue(t + 2, islot);
+        // Tile t - 1's keys (t + 3 selects its buffers; for t = 0 they are
+        // never offered).
+        float key[8];
+        keys(keep, t + 3, key);
+        const uint8_t* xl = ring + cslot * G::SLOT_BYTES + KP * (16 * G::HALF_CHUNKS) + col * CPR * 16;
         const int sw = col & SWZ;
-        f16v hh = {}, hl = {}, lh = {};
+        f16v acc = {};
 #pragma unroll
         for (int s = 0; s < NH; ++s) {
-            const int c = 4 * s + 2 * h;
+            const int c = 2 * s + h;
             const bf8v ah = __builtin_bit_cast(bf8v, *reinterpret_cast<const i4v*>(xl + 16 * (c ^ sw)));
-            const bf8v al = __builtin_bit_cast(bf8v, *reinterpret_cast<const i4v*>(xl + 16 * ((c + 1) ^ sw)));
-            hh = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, qh[s], hh, 0, 0, 0);
-            hl = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, ql[s], hl, 0, 0, 0);
-            lh = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, qh[s], lh, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, qh[s], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, ql[s], acc, 0, 0, 0);
         }
-        const f16v part = hh + (hl + lh);
-        // The k half as a constant (kp is uniform over the wave, so these
-        // are scalar branches): the previous tile's keys (its partner sums
-        // were published by this tile's barrier), then this tile's send.
-        if (kp == 0) {
-            if (t > 0) receive_and_offer(keep, t - 1, std::integral_constant<int, 0>());
-            send(part, t, keep, std::integral_constant<int, 0>());
-        } else {
-            if (t > 0) receive_and_offer(keep, t - 1, std::integral_constant<int, 1>());
-            send(part, t, keep, std::integral_constant<int, 1>());
-        }
+        if (t > 0) offer(key, t - 1);
+        send(acc, t, keep);
+        cslot = cslot == kBf2Slots - 1 ? 0 : cslot + 1;
+        islot = islot == kBf2Slots - 1 ? 0 : islot + 1;
     }
     if (ntiles > 0) {
-        __syncthreads();  // the last tile's partner sums and norms
-        if (kp == 0) receive_and_offer(keep, ntiles - 1, std::integral_constant<int, 0>());
-        else receive_and_offer(keep, ntiles - 1, std::integral_constant<int, 1>());
+        __syncthreads();  // the last tile's partner sums
+        float key[8];
+        keys(keep, ntiles - 1 + 4, key);
+        // Rows past the segment's end.
+        const int64_t left = seg1 - (seg0 + (int64_t)(ntiles - 1) * kGemmRows);
+        if (left < kGemmRows) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int v = 8 * KP + i;
+                const int m = 8 * (v >> 2) + 4 * h + (v & 3);
+                key[i] = m < left ? key[i] : __int_as_float(0x7F800000);
+            }
+        }
+        offer(key, ntiles - 1);
     }
     if (qvalid) {
-        uint64_t* out = ga.lists + (((size_t)qid * ga.nseg + seg) * kBf3Lists + 2 * kp + h) * C;
+        uint64_t* out = ga.lists + (((size_t)qid * ga.nseg + seg) * kBf2Lists + 2 * KP + h) * C;
 #pragma unroll
         for (int i = 0; i < C; ++i) out[i] = lst[i];
     }
 }
 
-// grid (1, nq): bound[q] = the kc-th smallest slot of the query's sampled
-// lists (kEmptySlot when they hold fewer than kc).
-__global__ __launch_bounds__(256) void lists_kth_slot(int kc, int64_t per_query,
-                                                      const uint64_t* __restrict__ lists,
-                                                      uint64_t* __restrict__ bound) {
+// grid: nseg * nqb blocks (1-D, XCD mapping as flat_gemm_f32); block 512.
+// hi_rows: the rows' bf16 high parts; wplane, cplane: per row w = sqrt(vn)
+// (1 / sqrt(vn) for cosine) and the remainder term without ||q|| (e' for
+// inner product and L2, e' / ||v|| for cosine); norms: vn; split_q: the
+// queries' split parts.
+template <int DIM, int METRIC, int C, bool BOUNDED>
+__global__ __launch_bounds__(512, 1) void flat_gemm_bf16x2(
+    const uint16_t* __restrict__ hi_rows, const float* __restrict__ wplane,
+    const float* __restrict__ cplane, const float* __restrict__ norms, int64_t n,
+    const uint32_t* __restrict__ split_q, const float* __restrict__ queries, int64_t nq,
+    BoundCoef bc, Bf2Args ga) {
+    // The k half is uniform over a wave: a scalar branch.
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (wave < 4)
+        bf2_segment<DIM, METRIC, C, BOUNDED, 0>(hi_rows, wplane, cplane, norms, n, split_q, queries,
+                                               nq, bc, ga, wave);
+    else
+        bf2_segment<DIM, METRIC, C, BOUNDED, 1>(hi_rows, wplane, cplane, norms, n, split_q, queries,
+                                               nq, bc, ga, wave);
+}
+
+// grid (1, nq), block 256: bound[q] = a slot with the key B and the largest
+// id, B the largest exact distance (host formulas, dots.c order) among the
+// k rows with the smallest keys in the query's sampled lists.  The k-th
+// smallest exact distance over all rows is at most B, so rows with keys
+// above B are not among the k nearest: the full launch admits only keys at
+// or below B.  kEmptySlot when the lists hold fewer than k rows.  Each
+// 16-lane group rescores rows with chain_dot (the merge's dots.c order).
+template <int NCH>
+__global__ __launch_bounds__(256) void lists_exact_bound(
+    int k, int64_t per_query, const uint64_t* __restrict__ lists, const float* __restrict__ rows,
+    const float* __restrict__ norms, int dim, const float* __restrict__ queries, int metric,
+    uint64_t* __restrict__ bound) {
     extern __shared__ uint64_t lds[];
+    __shared__ uint32_t s_ids[kGemmMaxKc];
+    __shared__ int s_cnt;
+    __shared__ uint32_t s_max;
+    const int tid = threadIdx.x, lr = tid & 15, grp = tid >> 4;
     const uint32_t q = blockIdx.y;
-    const uint64_t kth = block_kth_slot(lists + (size_t)q * per_query, per_query, kc, lds);
-    if (threadIdx.x == 0) bound[q] = kth;
+    const uint64_t* src = lists + (size_t)q * per_query;
+    const uint64_t kth = block_kth_slot(src, per_query, k, lds);
+    if (kth == kEmptySlot) {
+        if (tid == 0) bound[q] = kEmptySlot;
+        return;
+    }
+    if (tid == 0) {
+        s_cnt = 0;
+        s_max = 0;
+    }
+    __syncthreads();
+    // The lists hold each row at most once: exactly k slots are <= kth.
+    const bool in_lds = per_query <= kKthLdsSlots;
+    for (int64_t i = tid; i < per_query; i += blockDim.x) {
+        const uint64_t s = in_lds ? lds[i] : src[i];
+        if (s <= kth) s_ids[atomicAdd(&s_cnt, 1)] = slot_id(s);
+    }
+    __syncthreads();
+    const int dim4 = dim >> 2;
+    const float* qp = queries + (size_t)q * dim;
+    f4v qv[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const int idx = lr + 16 * c;
+        qv[c] = idx < dim4 ? *reinterpret_cast<const f4v*>(qp + 4 * idx) : f4v{0.f, 0.f, 0.f, 0.f};
+    }
+    const float qn = metric == kMetricIP ? 0.0f : chain_dot<NCH>(qv, qv, dim4);
+    const int cnt = s_cnt;
+    for (int j = grp; j < cnt; j += 16) {
+        const uint32_t id = s_ids[j];
+        const float* rp = rows + (size_t)id * dim;
+        f4v rv[NCH];
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const int idx = lr + 16 * c;
+            rv[c] = idx < dim4 ? *reinterpret_cast<const f4v*>(rp + 4 * idx) : f4v{0.f, 0.f, 0.f, 0.f};
+        }
+        const float dot = chain_dot<NCH>(qv, rv, dim4);
+        if (lr == 0) atomicMax(&s_max, ordered_bits(host_distance(dot, qn, norms[id], metric)));
+    }
+    __syncthreads();
+    if (tid == 0) bound[q] = ((uint64_t)s_max << 32) | 0xFFFFFFFFull;
 }
 
 // grid (1, nq): one block per query selects the kc smallest keys over its
@@ -752,95 +928,123 @@ size_t gemm_lists_bytes(const GemmPlan& p, int64_t nq) {
 }
 
 // Unit roundoff for make_bounds that covers the split-bf16 dot error
-// g = 1.024 gamma_d(2^-23) + 3.01 2^-16 + 2^-21 (gamma_d(u_eff) = g).
-static double bf3_unit_roundoff(int dim) {
+// without the rows' remainder term: one accumulation chain of 2 d products
+// (d / 2 k values, two products each, per half, then the halves added: at
+// most d + 1 roundings per product), so
+// g = 1.024 gamma_{d+1}(2^-23) + 1.01 2^-16 + 2^-22 (gamma_d(u_eff) = g).
+static double bf2_unit_roundoff(int dim) {
     const double u23 = 1.0 / 8388608.0;
-    const double gd = dim * u23 / (1.0 - dim * u23);
-    const double g = 1.024 * gd + 3.01 / 65536.0 + 1.0 / 2097152.0;
+    const double gd = (dim + 1) * u23 / (1.0 - (dim + 1) * u23);
+    const double g = 1.024 * gd + 1.01 / 65536.0 + 1.0 / 4194304.0;
     return g / ((double)dim * (1.0 + g));
 }
 
+struct Bf2Inputs {
+    const uint16_t* hi_rows;
+    const float* wplane;
+    const float* cplane;
+    const float* norms;
+    int64_t n;
+    const uint32_t* split_q;
+    const float* queries;
+    int64_t nq;
+};
+
 template <int DIM, int C, bool BOUNDED>
-static void launch_bf3_dim_c(const GemmPlan& p, const uint32_t* split_rows, const float* norms,
-                             int64_t n, const uint32_t* split_q, const float* queries, int64_t nq,
-                             int metric, const Bf3Args& ga, hipStream_t s) {
-    const BoundCoef bc = make_bounds(DIM, bf3_unit_roundoff(DIM));
+static void launch_bf2_dim_c(const GemmPlan& p, const Bf2Inputs& in, int metric, const Bf2Args& ga,
+                             hipStream_t s) {
+    const BoundCoef bc = make_bounds(DIM, bf2_unit_roundoff(DIM));
     const dim3 grid((unsigned)(ga.nseg * p.nqb));
-    const size_t shmem = bf3_lds_bytes<DIM>();
+    const size_t shmem = bf2_lds_bytes<DIM>();
     static bool attr = [] {
-        (void)hipFuncSetAttribute((const void*)flat_gemm_bf16x3<DIM, kMetricCosine, C, BOUNDED>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)bf3_lds_bytes<DIM>());
-        (void)hipFuncSetAttribute((const void*)flat_gemm_bf16x3<DIM, kMetricL2, C, BOUNDED>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)bf3_lds_bytes<DIM>());
-        (void)hipFuncSetAttribute((const void*)flat_gemm_bf16x3<DIM, kMetricIP, C, BOUNDED>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)bf3_lds_bytes<DIM>());
+        (void)hipFuncSetAttribute((const void*)flat_gemm_bf16x2<DIM, kMetricCosine, C, BOUNDED>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)bf2_lds_bytes<DIM>());
+        (void)hipFuncSetAttribute((const void*)flat_gemm_bf16x2<DIM, kMetricL2, C, BOUNDED>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)bf2_lds_bytes<DIM>());
+        (void)hipFuncSetAttribute((const void*)flat_gemm_bf16x2<DIM, kMetricIP, C, BOUNDED>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)bf2_lds_bytes<DIM>());
         return true;
     }();
     (void)attr;
-    const dim3 block(64 * kBf3Waves);
+    const dim3 block(64 * kBf2Waves);
     switch (metric) {
     case kMetricCosine:
-        hipLaunchKernelGGL((flat_gemm_bf16x3<DIM, kMetricCosine, C, BOUNDED>), grid, block, shmem,
-                           s, split_rows, norms, n, split_q, queries, nq, bc, ga);
+        hipLaunchKernelGGL((flat_gemm_bf16x2<DIM, kMetricCosine, C, BOUNDED>), grid, block, shmem,
+                           s, in.hi_rows, in.wplane, in.cplane, in.norms, in.n, in.split_q, in.queries, in.nq, bc, ga);
         break;
     case kMetricL2:
-        hipLaunchKernelGGL((flat_gemm_bf16x3<DIM, kMetricL2, C, BOUNDED>), grid, block, shmem, s,
-                           split_rows, norms, n, split_q, queries, nq, bc, ga);
+        hipLaunchKernelGGL((flat_gemm_bf16x2<DIM, kMetricL2, C, BOUNDED>), grid, block, shmem, s,
+                           in.hi_rows, in.wplane, in.cplane, in.norms, in.n, in.split_q, in.queries, in.nq, bc, ga);
         break;
     default:
-        hipLaunchKernelGGL((flat_gemm_bf16x3<DIM, kMetricIP, C, BOUNDED>), grid, block, shmem, s,
-                           split_rows, norms, n, split_q, queries, nq, bc, ga);
+        hipLaunchKernelGGL((flat_gemm_bf16x2<DIM, kMetricIP, C, BOUNDED>), grid, block, shmem, s,
+                           in.hi_rows, in.wplane, in.cplane, in.norms, in.n, in.split_q, in.queries, in.nq, bc, ga);
         break;
     }
 }
 
 template <int DIM>
-static void launch_bf3_dim(const GemmPlan& p, bool bounded, const uint32_t* split_rows,
-                           const float* norms, int64_t n, const uint32_t* split_q,
-                           const float* queries, int64_t nq, int metric, const Bf3Args& ga,
-                           hipStream_t s) {
+static void launch_bf2_dim(const GemmPlan& p, bool bounded, const Bf2Inputs& in, int metric,
+                           const Bf2Args& ga, hipStream_t s) {
     if (gemm_list_len(p.kc) == 4) {
-        if (bounded) launch_bf3_dim_c<DIM, 4, true>(p, split_rows, norms, n, split_q, queries, nq, metric, ga, s);
-        else launch_bf3_dim_c<DIM, 4, false>(p, split_rows, norms, n, split_q, queries, nq, metric, ga, s);
+        if (bounded) launch_bf2_dim_c<DIM, 4, true>(p, in, metric, ga, s);
+        else launch_bf2_dim_c<DIM, 4, false>(p, in, metric, ga, s);
     } else {
-        if (bounded) launch_bf3_dim_c<DIM, 8, true>(p, split_rows, norms, n, split_q, queries, nq, metric, ga, s);
-        else launch_bf3_dim_c<DIM, 8, false>(p, split_rows, norms, n, split_q, queries, nq, metric, ga, s);
+        if (bounded) launch_bf2_dim_c<DIM, 8, true>(p, in, metric, ga, s);
+        else launch_bf2_dim_c<DIM, 8, false>(p, in, metric, ga, s);
     }
 }
 
-hipError_t launch_flat_bf3(const GemmPlan& p, bool sampled, const uint32_t* split_rows,
-                           const float* norms, int64_t n, int dim, const uint32_t* split_q,
+hipError_t launch_flat_bf2(const GemmPlan& p, bool sampled, const uint16_t* hi_rows,
+                           const float* recs, const float* norms, int64_t n, int dim,
+                           const uint32_t* split_q,
                            const float* queries, int64_t nq, int metric, const uint64_t* qbound,
                            uint64_t* lists, hipStream_t s) {
-    Bf3Args ga;
+    Bf2Args ga;
     ga.nseg = sampled ? p.s_nseg : p.nseg;
     ga.nqb = p.nqb;
     ga.rows_per_seg = sampled ? p.s_rows_per_seg : p.rows_per_seg;
     ga.seg_rows = sampled ? p.s_seg_rows : p.rows_per_seg;
-    // Products and partial sums of three chains flushed below 2^-126,
-    // counted twice for L2's -2 dot.
+    // Products and partial sums flushed below 2^-126 (fewer than 6 dim of
+    // them per dot), counted twice for L2's -2 dot.
     ga.abs_slack = (float)(12.0 * dim * 1.1754943508222875e-38);
     ga.qbound = qbound;
     ga.lists = lists;
     const bool bounded = !sampled;
+    // The planes of the metric: [4][n] = cosine w, cosine c, L2 and inner
+    // product w, L2 and inner product c.
+    const float* wp = recs + (metric == kMetricCosine ? 0 : 2 * n);
+    const Bf2Inputs in{hi_rows, wp, wp + n, norms, n, split_q, queries, nq};
     switch (dim) {
-    case 64: launch_bf3_dim<64>(p, bounded, split_rows, norms, n, split_q, queries, nq, metric, ga, s); break;
-    case 96: launch_bf3_dim<96>(p, bounded, split_rows, norms, n, split_q, queries, nq, metric, ga, s); break;
-    case 128: launch_bf3_dim<128>(p, bounded, split_rows, norms, n, split_q, queries, nq, metric, ga, s); break;
-    case 192: launch_bf3_dim<192>(p, bounded, split_rows, norms, n, split_q, queries, nq, metric, ga, s); break;
-    case 256: launch_bf3_dim<256>(p, bounded, split_rows, norms, n, split_q, queries, nq, metric, ga, s); break;
-    case 384: launch_bf3_dim<384>(p, bounded, split_rows, norms, n, split_q, queries, nq, metric, ga, s); break;
+    case 64: launch_bf2_dim<64>(p, bounded, in, metric, ga, s); break;
+    case 96: launch_bf2_dim<96>(p, bounded, in, metric, ga, s); break;
+    case 128: launch_bf2_dim<128>(p, bounded, in, metric, ga, s); break;
+    case 192: launch_bf2_dim<192>(p, bounded, in, metric, ga, s); break;
+    case 256: launch_bf2_dim<256>(p, bounded, in, metric, ga, s); break;
+    case 384: launch_bf2_dim<384>(p, bounded, in, metric, ga, s); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 
-hipError_t launch_bf3_bounds(const GemmPlan& p, int64_t nq, const uint64_t* lists, uint64_t* bound,
-                             hipStream_t s) {
-    const int64_t per_query = (int64_t)p.s_nseg * kBf3Lists * gemm_list_len(p.kc);
-    hipLaunchKernelGGL(lists_kth_slot, dim3(1, (unsigned)nq), dim3(256),
-                       per_query <= kKthLdsSlots ? sizeof(uint64_t) * (size_t)per_query : 0, s, p.kc,
-                       per_query, lists, bound);
+hipError_t launch_bf2_bounds(const GemmPlan& p, int64_t nq, int k, const uint64_t* lists,
+                             const float* rows, const float* norms, int dim, const float* queries,
+                             int metric, uint64_t* bound, hipStream_t s) {
+    const int64_t per_query = (int64_t)p.s_nseg * kBf2Lists * gemm_list_len(p.kc);
+    const size_t shmem = per_query <= kKthLdsSlots ? sizeof(uint64_t) * (size_t)per_query : 0;
+    const dim3 grid(1, (unsigned)nq);
+#define MANS_BOUND_CASE(N)                                                                       \
+    hipLaunchKernelGGL(lists_exact_bound<N>, grid, dim3(256), shmem, s, k, per_query, lists, rows, \
+                       norms, dim, queries, metric, bound)
+    switch (flat_nch_for_dim(dim)) {
+    case 1: MANS_BOUND_CASE(1); break;
+    case 2: MANS_BOUND_CASE(2); break;
+    case 3: MANS_BOUND_CASE(3); break;
+    case 4: MANS_BOUND_CASE(4); break;
+    case 6: MANS_BOUND_CASE(6); break;
+    default: return hipErrorInvalidValue;
+    }
+#undef MANS_BOUND_CASE
     return hipGetLastError();
 }
 

@@ -70,20 +70,29 @@ hipError_t launch_flat_gemm_merge(const GemmPlan& p, const float* rows, const fl
                                   hipStream_t s);
 
 // Split-bf16 contraction (fp32-level accuracy on bf16 MFMA).
-// Splits `count` rows of dim floats into [8 hi | 8 lo] bf16 parts per 8
-// elements; bad[row] (per_row) or bad[0] is or-ed with 1 for a value
-// outside [2^-50, 2^50] (other than 0).
-hipError_t launch_split_bf16(const float* src, int64_t count, int dim, uint32_t* dst,
-                             uint32_t* bad, bool per_row, hipStream_t s);
+// Splits `count` queries of dim floats into [8 hi | 8 lo] bf16 parts per 8
+// elements; bad[query] is or-ed with 1 for a value outside [2^-50, 2^50]
+// (other than 0).
+hipError_t launch_split_queries(const float* src, int64_t count, int dim, uint32_t* dst,
+                                uint32_t* bad, hipStream_t s);
+// Rows: hi gets the bf16 high parts ([count][dim]), recs four per-row
+// planes ([4][count] floats: the cosine keys' w and c, then those of L2 and
+// inner product) from the rows and their squared norms; bad[0] is or-ed
+// with 1 for a value outside the range.
+hipError_t launch_split_rows(const float* src, const float* norms, int64_t count, int dim,
+                             uint16_t* hi, float* recs, uint32_t* bad, hipStream_t s);
 // sampled: the bounding launch (no bounds); otherwise the full launch with
 // the per-query bounds qbound.  Writes the lane lists.
-hipError_t launch_flat_bf3(const GemmPlan& p, bool sampled, const uint32_t* split_rows,
-                           const float* norms, int64_t n, int dim, const uint32_t* split_q,
+hipError_t launch_flat_bf2(const GemmPlan& p, bool sampled, const uint16_t* hi_rows,
+                           const float* recs, const float* norms, int64_t n, int dim,
+                           const uint32_t* split_q,
                            const float* queries, int64_t nq, int metric, const uint64_t* qbound,
                            uint64_t* lists, hipStream_t s);
-// bound[q] = the kc-th smallest slot of the sampled lists of query q.
-hipError_t launch_bf3_bounds(const GemmPlan& p, int64_t nq, const uint64_t* lists, uint64_t* bound,
-                             hipStream_t s);
+// bound[q]: from the sampled lists of query q, a slot whose key is the
+// largest exact distance among the k rows with the smallest keys.
+hipError_t launch_bf2_bounds(const GemmPlan& p, int64_t nq, int k, const uint64_t* lists,
+                             const float* rows, const float* norms, int dim, const float* queries,
+                             int metric, uint64_t* bound, hipStream_t s);
 
 // target_blocks: blocks over all queries of a launch (0: the flat scan's default).
 FlatPlan plan_flat(int64_t n, int64_t nq, int kc, int64_t target_blocks = 0);

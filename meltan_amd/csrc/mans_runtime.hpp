@@ -98,11 +98,12 @@ struct mans_corpus {
     // int8 planes (Int8CodeCache.swift:22-108), built on first use.
     bool int8_valid = false;
     mans::DevBuf i8_codes, i8_u, i8_w, i8_normsq, i8_invsqrt;
-    // Split-bf16 parts of the rows for the batched contraction, built on
-    // first use; bf_ok: every value is in the split range.
+    // The rows' bf16 high parts ([n][dim]) and key planes ([4][n] floats)
+    // for the batched split-bf16 contraction, built on first use; bf_ok:
+    // every value is in the split range.
     bool bf_valid = false;
     bool bf_ok = false;
-    mans::DevBuf bf_split, bf_flag;
+    mans::DevBuf bf_hi, bf_rec, bf_flag;
 };
 
 namespace mans {

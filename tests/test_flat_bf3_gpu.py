@@ -1,9 +1,11 @@
 """Parity of the batched flat path on split-bf16 MFMA.
 
 Batches of at least 16 queries with k <= 32 run the contraction on
-v_mfma_f32_32x32x16_bf16 with every value split into two bf16 parts (three
-partial products).  Its keys are lower bounds with the split's error
-included, so the results must meet the streaming scan's bar: distances
+v_mfma_f32_32x32x16_bf16 with the queries split into two bf16 parts and the
+rows kept as their bf16 high parts plus the norm of the remainder (two
+partial products).  Its keys are lower bounds with the split's error and
+the rows' remainder term included, so the results must meet the streaming
+scan's bar: distances
 bit-identical to the oracle's (dots.c order, host formulas), ids equal
 except on exact ties.  A corpus with values outside the split range keeps
 the fp32 contraction; a query outside it is re-run by the streaming scan.
