@@ -202,15 +202,16 @@ def bench_flat(args, ctx):
         reps = min(steps, 20)
         kt = kernel_avg(ctx, step, reps, ["flat_bound", "flat_gemm", "flat_merge", "flat_scan"], hip)
         if kt["flat_gemm"][1] and kt["flat_bound"][1]:
-            # Split-bf16 contraction: three bf16 MFMA products per fp32
-            # product.  achieved = algorithmic flops (2 B n d) / launch time
-            # against the dense bf16 peak; the issued rate is three times it.
+            # Split-bf16 contraction: two bf16 MFMA products per fp32
+            # product (query hi and lo parts against the row's hi part).
+            # achieved = algorithmic flops (2 B n d) / launch time against
+            # the dense bf16 peak; the issued rate is twice it.
             avg, launches = kt["flat_gemm"]
             flops = 2.0 * (b * reps / launches) * n * dim
-            roof = roofline_mfma("flat_gemm_bf16x3<384,cosine,4,bounded>", f"flat_{n}x{dim}_b{b}",
+            roof = roofline_mfma("flat_gemm_bf16x2<384,cosine,8,bounded>", f"flat_{n}x{dim}_b{b}",
                                  flops, avg, peak=BF16_MFMA_TFLOPS)
-            roof["issued_tflops"] = round(3 * flops / avg / 1e12, 2)
-            roof["issued_frac"] = round(3 * flops / avg / 1e12 / BF16_MFMA_TFLOPS, 4)
+            roof["issued_tflops"] = round(2 * flops / avg / 1e12, 2)
+            roof["issued_frac"] = round(2 * flops / avg / 1e12 / BF16_MFMA_TFLOPS, 4)
             roof["bound_pass_us"] = round(kt["flat_bound"][0] * 1e6, 2)
             roof["merge_avg_us"] = round(kt["flat_merge"][0] * 1e6, 2) if kt["flat_merge"][1] else None
         elif kt["flat_gemm"][1]:

@@ -762,7 +762,7 @@ static int bf16_split_ensure(mans_ctx* ctx, const mans_corpus* cc, hipStream_t s
         return MANS_OK;
     }
     hipError_t e = c->bf_hi.ensure((size_t)c->n * c->dim * sizeof(uint16_t), ctx->fail_alloc);
-    if (e == hipSuccess) e = c->bf_rec.ensure((size_t)c->n * 4 * sizeof(float), ctx->fail_alloc);
+    if (e == hipSuccess) e = c->bf_rec.ensure((size_t)c->n * 8 * sizeof(float), ctx->fail_alloc);
     if (e == hipSuccess) e = c->bf_flag.ensure(sizeof(uint32_t), ctx->fail_alloc);
     if (e == hipSuccess) e = hipMemsetAsync(c->bf_flag.p, 0, sizeof(uint32_t), st);
     if (e == hipSuccess)
@@ -867,16 +867,16 @@ static int flat_search_chunk(mans_ctx* ctx, const mans_corpus* c, const float* d
                 if (e == hipSuccess)
                     e = launch_split_queries(d_q, npend, dim, qs, (uint32_t*)slot->qbad.p, st);
                 if (e == hipSuccess)
-                    e = launch_flat_bf2(gp, true, hi, rec, norms, n, dim, qs, d_q, npend,
-                                        (int)metric, nullptr, lists, st);
+                    e = launch_flat_bf2(gp, true, hi, rec, n, dim, qs, d_q, npend, (int)metric,
+                                        nullptr, lists, nullptr, st);
                 if (e == hipSuccess)
                     e = launch_bf2_bounds(gp, npend, keff, lists, rows, norms, dim, d_q,
                                           (int)metric, qbound, st);
                 ctx->time_end(slot, st, "flat_bound");
                 ctx->time_begin(slot, st);
                 if (e == hipSuccess)
-                    e = launch_flat_bf2(gp, false, hi, rec, norms, n, dim, qs, d_q, npend,
-                                        (int)metric, qbound, lists, st);
+                    e = launch_flat_bf2(gp, false, hi, rec, n, dim, qs, d_q, npend, (int)metric,
+                                        qbound, lists, (uint32_t*)slot->qbad.p, st);
                 ctx->time_end(slot, st, "flat_gemm");
             } else {
                 ctx->time_begin(slot, st);

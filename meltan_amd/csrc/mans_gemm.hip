@@ -337,11 +337,11 @@ hipError_t launch_split_queries(const float* src, int64_t count, int dim, uint32
 }
 
 // One wave per row of `count` rows of dim (multiple of 8) floats: hi gets
-// the row's bf16 high parts and recs four planes of `count` floats:
-// 1 / sqrt(vn) and e' / sqrt(vn) (cosine), sqrt(vn) and e' (L2, inner
-// product), with vn the row's squared norm and e' >= (1 + 2^-12) ||v - vh||
-// (summed in double, rounded up); bad[0] gets 1 for a value outside the
-// range.
+// the row's bf16 high parts and recs two record planes of `count` float4s:
+// {vn, 1 / sqrt(vn), e' / sqrt(vn), 0} (cosine) and {vn, sqrt(vn), e', 0}
+// (L2, inner product), with vn the row's squared norm and
+// e' >= (1 + 2^-12) ||v - vh|| (summed in double, rounded up); bad[0] gets
+// 1 for a value outside the range.
 __global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict__ src,
                                                          const float* __restrict__ norms,
                                                          int64_t count, int dim,
@@ -384,10 +384,9 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict
         const float vn = norms[row];
         const float ws = sqrtf(vn);
         const float wr = vn > 0.0f ? 1.0f / ws : 0.0f;
-        recs[row] = wr;
-        recs[count + row] = f * wr;
-        recs[2 * count + row] = ws;
-        recs[3 * count + row] = f;
+        f4v* r4 = reinterpret_cast<f4v*>(recs);
+        r4[row] = f4v{vn, wr, f * wr, 0.0f};
+        r4[count + row] = f4v{vn, ws, f, 0.0f};
     }
     if (!ok) atomicOr(bad, 1u);
 }
@@ -401,65 +400,6 @@ hipError_t launch_split_rows(const float* src, const float* norms, int64_t count
 }
 
 typedef __bf16 bf8v __attribute__((ext_vector_type(8)));
-
-// Work split.  A block of 8 waves serves 128 queries over one segment of
-// rows: wave w takes query group w & 3 (32 queries) and half w >> 2 of the
-// k range, so a wave keeps only its half of the query's split parts in
-// registers and two waves fit on a SIMD (one hides the other's latencies).
-// Per 32-row tile the two halves' sums are exchanged through LDS and added
-// (the same IEEE sum in either wave), and each wave keys 8 of the 16 rows a
-// lane holds, keeping its own lane lists (4 lists per query and segment:
-// half x lane half).
-//
-// Tiles reach LDS by direct global-to-LDS loads (global_load_lds, 16 bytes
-// per lane) into a ring of three slots, two tiles ahead, without holding
-// registers.  A slot holds, per k half, 32 rows x CPR 16-byte chunks
-// unpadded; chunk c of row r sits at c ^ (r & SWZ), so the lanes of a
-// half-wave reading one chunk of 32 rows spread over the banks.  Each wave
-// issues the same number of row loads per tile (a tile that does not split
-// evenly over the block's lanes is padded) and wave 0 one more, the tile's
-// row records, into a ring of four record slots; so a wave waits for tile t
-// while tile t + 1's loads stay in flight.
-//
-// Per iteration t a wave computes the keys of tile t - 1 (branch-free, in
-// the same block as tile t's MFMAs so the scheduler can place them between
-// them), then tile t's MFMAs, then the insertion path for tile t - 1's keys
-// at or below the lane's threshold, then sends tile t's partner half.
-constexpr int kBf2Waves = 8;
-constexpr int kBf2Slots = 3;
-constexpr int kBf2RecSlots = 4;
-constexpr int kBf2Lists = 4;  // lane lists per query and segment
-
-template <int DIM>
-struct Bf2Shape {
-    static constexpr int NS = DIM / 16;  // MFMA k-steps per row
-    static constexpr int NH = NS / 2;    // k-steps per half
-    static constexpr int CPR = 2 * NH;   // 16-byte chunks of a row per half
-    static constexpr int LOWBIT = CPR & -CPR;
-    static constexpr int SWZ = (LOWBIT < 16 ? LOWBIT : 16) - 1;
-    static constexpr int HALF_CHUNKS = kGemmRows * CPR;
-    static constexpr int TILE_CHUNKS = 2 * HALF_CHUNKS;
-    static constexpr int LOADS = (TILE_CHUNKS + 64 * kBf2Waves - 1) / (64 * kBf2Waves);
-    static constexpr int SLOT_BYTES = 16 * 64 * kBf2Waves * LOADS;
-    static_assert(DIM % 32 == 0, "unsupported dimension");
-};
-
-template <int DIM>
-size_t bf2_lds_bytes() {
-    return kBf2Slots * (size_t)Bf2Shape<DIM>::SLOT_BYTES +
-           sizeof(float) * (kBf2RecSlots * 3 * kGemmRows + 2 * kBf2Waves * 64 * 8);
-}
-
-struct Bf2Args {
-    int nseg;
-    int nqb;
-    int64_t rows_per_seg;     // multiple of kGemmRows
-    int64_t seg_rows;         // rows scanned from each segment's start
-    float abs_slack;
-    const uint64_t* qbound;   // per query (BOUNDED)
-    uint64_t* lists;          // [nq][nseg][kBf2Lists][C]
-};
-
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 // s_waitcnt vmcnt(N) through the builtin, so the compiler's own wait
@@ -471,24 +411,116 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+constexpr int kBf2Waves = 8;
+constexpr int kBf2Slots = 3;     // row tile ring: tile t + 2 loads while tile t is used
+constexpr int kBf2RecSlots = 4;  // row record ring
+constexpr int kBf2Lists = 4;     // sampled launch: lane lists per query and segment
+constexpr int kBf2Cap = 32;      // full launch: candidate slots per query and segment
+// The full launch's 32 x 32 sums of a query group, query-major: query q's
+// 32 rows start at q * kBf2DotStride + (q / 16) * 32 floats (16-byte
+// aligned; the key waves' two query halves fall on different banks).
+constexpr int kBf2DotStride = 36;
+constexpr int kBf2DotGroup = 32 * kBf2DotStride + 32;
+
+// The chunk permutation of row r in a tile whose rows are cpr 16-byte
+// chunks: chunk c sits at c ^ bf2_swz(r).  With a row stride of 8 chunks
+// mod 16 (128 bytes mod 256), rows r and r + 1 fall in different 128-byte
+// halves, so (r / 2) & 7 keeps the 16 rows read by 16 lanes at 16 distinct
+// 16-byte bank groups; otherwise r & swz with swz + 1 the largest power of
+// two (at most 16) dividing cpr.
+template <int CPR>
+struct Bf2Swizzle {
+    static constexpr int LOWBIT = CPR & -CPR;
+    static constexpr int SWZ = (CPR & 15) == 8 ? 7 : (LOWBIT < 16 ? LOWBIT : 16) - 1;
+    __device__ static int of(int r) { return (CPR & 15) == 8 ? (r >> 1) & 7 : r & SWZ; }
+};
+
+// ---------------------------------------------------------------------------
+// Work split: 8 waves serve 128 queries over one segment of rows; wave w
+// takes query group w & 3 (32 queries) and half w >> 2 of the k range, so a
+// wave keeps only its half of the query's split parts in registers and two
+// waves fit on a SIMD.  Per 32-row tile the two halves' sums are exchanged
+// through LDS and added (the same IEEE sum in either wave), and each wave
+// keys 8 of the 16 rows a lane holds.  The sampled launch (no bounds)
+// inserts them into sorted lane lists (4 lists per query and segment: half
+// x lane half), lowering each lane's threshold as its list fills; the full
+// launch appends keys at or below the query's bound to a candidate buffer
+// per query and segment.
+//
+// Tiles reach LDS by direct global-to-LDS loads (global_load_lds, 16 bytes
+// per lane) into a ring of three slots, two tiles ahead; each wave issues
+// the same number of row loads per tile (padded) and wave 0 one more, the
+// tile's row records.  A slot holds, per k half, 32 rows x CPR swizzled
+// 16-byte chunks.
+template <int DIM>
+struct Bf2Shape {
+    static constexpr int NS = DIM / 16;  // MFMA k-steps per row
+    static constexpr int NH = NS / 2;    // k-steps per half
+    static constexpr int CPR = 2 * NH;   // 16-byte chunks of a row per half
+    using Swz = Bf2Swizzle<CPR>;
+    static constexpr int HALF_CHUNKS = kGemmRows * CPR;
+    static constexpr int TILE_CHUNKS = 2 * HALF_CHUNKS;
+    static constexpr int LOADS = (TILE_CHUNKS + 64 * kBf2Waves - 1) / (64 * kBf2Waves);
+    static constexpr int SLOT_BYTES = 16 * 64 * kBf2Waves * LOADS;
+    static_assert(DIM % 32 == 0, "unsupported dimension");
+};
+
+template <int DIM>
+constexpr size_t bf2_lds_bytes() {
+    return kBf2Slots * (size_t)Bf2Shape<DIM>::SLOT_BYTES + 16 * kBf2RecSlots * kGemmRows +
+           16 * 2 * 2 * kBf2Waves * 64;
+}
+
+struct Bf2Args {
+    int nseg;
+    int nqb;
+    int64_t rows_per_seg;     // multiple of kGemmRows
+    int64_t seg_rows;         // rows scanned from each segment's start
+    float abs_slack;
+    const uint64_t* qbound;   // full launch: per query
+    // Sampled launch: lane lists [nq][nseg][kBf2Lists][C].  Full launch:
+    // candidate buffers [nq][nseg][kBf2Cap], unsorted, padded with
+    // kEmptySlot; a buffer that fills up sets bit 2 of qflag[query].
+    uint64_t* lists;
+    uint32_t* qflag;
+};
+
+// The lower-bound key of a row from its dot f with the query (the split
+// contraction's sum), the query's qn, sqrt(qn), 1 / sqrt(qn) and cosine
+// threshold vn_tiny, and the row's record {vn, w, c, 0}.
+template <int METRIC>
+__device__ __forceinline__ float bf2_key(float f, float qn, float sq, float rq, float vn_tiny,
+                                         const f4v& rec, const BoundCoef& bc, float eps_all,
+                                         float abs_slack) {
+    const float vn = rec.x, wv = rec.y, vc = rec.z;
+    if (METRIC == kMetricIP) return (-f - sq * (wv * bc.c_ip + vc)) - abs_slack;
+    if (METRIC == kMetricL2) {
+        float dd = qn - 2.0f * f + vn;
+        dd = dd > 0.0f ? dd : 0.0f;
+        return (dd - ((qn + vn + 2.0f * (sq * wv)) * bc.c_l2 + sq * (2.0f * vc))) - abs_slack;
+    }
+    // A zero row has wv = vc = 0 and key 1 - eps (both paths give exactly
+    // 1); rows with qn vn below 1.03e-20 get -1 (the formula's 1e-10 branch
+    // is near).
+    const float k = (1.0f - f * (rq * wv)) - (eps_all + vc);
+    return vn < vn_tiny ? -1.0f : k;
+}
+
 // One wave's work over the block's segment; KP: the wave's k half.
 template <int DIM, int METRIC, int C, bool BOUNDED, int KP>
 __device__ __forceinline__ void bf2_segment(const uint16_t* __restrict__ hi_rows,
-                                            const float* __restrict__ wplane,
-                                            const float* __restrict__ cplane,
-                                            const float* __restrict__ norms, int64_t n,
-                                            const uint32_t* __restrict__ split_q,
-                                            const float* __restrict__ queries, int64_t nq,
-                                            const BoundCoef& bc, const Bf2Args& ga, int wave) {
+                                                    const f4v* __restrict__ recs, int64_t n,
+                                                    const uint32_t* __restrict__ split_q,
+                                                    const float* __restrict__ queries, int64_t nq,
+                                                    const BoundCoef& bc, const Bf2Args& ga,
+                                                    int wave) {
     using G = Bf2Shape<DIM>;
-    constexpr int NH = G::NH, CPR = G::CPR, SWZ = G::SWZ;
+    constexpr int NH = G::NH, CPR = G::CPR;
     extern __shared__ uint64_t lds[];
-    uint8_t* ring = reinterpret_cast<uint8_t*>(lds);  // [slot][half][32][CPR][16]
-    // Per record slot: w[32], c[32], vn[32].
-    float* trec = reinterpret_cast<float*>(ring + kBf2Slots * G::SLOT_BYTES);
-    // Partner sums: [2][wave][64] f4v, first and second four.
-    f4v* xa = reinterpret_cast<f4v*>(trec + kBf2RecSlots * 3 * kGemmRows);
-    f4v* xb = xa + 2 * kBf2Waves * 64;
+    uint8_t* ring = reinterpret_cast<uint8_t*>(lds);                       // [slot][half][32][CPR][16]
+    f4v* trec = reinterpret_cast<f4v*>(ring + kBf2Slots * G::SLOT_BYTES);  // [rec slot][32]
+    f4v* xa = trec + kBf2RecSlots * kGemmRows;  // partner sums [2][wave][64], first four
+    f4v* xb = xa + 2 * kBf2Waves * 64;          // and second four
     const int lane = threadIdx.x & 63;
     const int qg = wave & 3;
     const int h = lane >> 5, col = lane & 31;
@@ -523,16 +555,18 @@ __device__ __forceinline__ void bf2_segment(const uint16_t* __restrict__ hi_rows
     const float qn = qsq + __shfl_xor(qsq, 32);
     const float sq = sqrtf(qn);
     const float rq = 1.0f / sq;
-    // Cosine rows with qn vn below 1.03e-20 get the key -1 (the formula's
-    // 1e-10 branch is near); vn below this threshold covers every such row.
     const float vn_tiny = (1.03e-20f / qn) * 1.0001f;
     const float eps_all = bc.eps_cos + ga.abs_slack;
     uint64_t lst[C];
 #pragma unroll
     for (int i = 0; i < C; ++i) lst[i] = kEmptySlot;
-    const uint64_t bound = !qvalid ? 0ull : (BOUNDED ? ga.qbound[qid] : kEmptySlot);
+    const uint64_t bound = BOUNDED && qvalid ? ga.qbound[qid] : kEmptySlot;
     float thr = !qvalid ? -__int_as_float(0x7F800000)
                         : (bound == kEmptySlot ? __int_as_float(0x7F800000) : slot_key(bound));
+    // Full launch: candidates so far in this query's region for this k
+    // half (the same in the query's two lanes).
+    uint32_t cnt = 0;
+    uint64_t* region = ga.lists + ((size_t)qrow * ga.nseg + seg) * kBf2Cap + KP * (kBf2Cap / 2);
 
     const int64_t seg0 = (int64_t)seg * ga.rows_per_seg;
     const int64_t seg1 = seg0 + ga.seg_rows < n ? seg0 + ga.seg_rows : n;
@@ -549,19 +583,15 @@ __device__ __forceinline__ void bf2_segment(const uint16_t* __restrict__ hi_rows
         p = p < G::TILE_CHUNKS ? p : 0;
         const int half = p / G::HALF_CHUNKS, rem = p - half * G::HALF_CHUNKS;
         const int r = rem / CPR, qq = rem - r * CPR;
-        const int c = qq ^ (r & SWZ);
+        const int c = qq ^ G::Swz::of(r);
         vrow[u] = r;
         voff[u] = (uint32_t)(r * DIM * 2 + half * (16 * CPR) + 16 * c);
     }
     const uint8_t* seg_base = reinterpret_cast<const uint8_t*>(hi_rows + seg0 * DIM);
-    // Waves 0, 1 and 2 load a tile's w, c and vn planes.
-    const float* plane = wave == 0 ? wplane : (wave == 1 ? cplane : norms);
-    // The query parts and the bound are in registers before the first tile
-    // loads are issued.
-    wait_vmcnt<0>();
+    wait_vmcnt<0>();  // the query parts, before the first tile loads
 
-    // Loads tile t into ring slot `slot` (both k halves) and its record
-    // planes into record slot t % 4.  Rows past the segment's end load its
+    // Loads tile t into ring slot `slot` (both k halves) and (wave 0) its
+    // records into record slot t % 4.  Rows past the segment's end load its
     // last row.
     auto issue = [&](int t, int slot) {
         if (t >= ntiles) return;
@@ -580,16 +610,15 @@ __device__ __forceinline__ void bf2_segment(const uint16_t* __restrict__ hi_rows
                                                  (lds_ptr_t)(dst + u * 1024), 16, 0, 0);
             }
         }
-        if (wave < 3) {
+        if (wave == 0) {
             int64_t row = seg0 + (int64_t)t * kGemmRows + (lane & 31);
             row = row < seg1 ? row : seg1 - 1;
             if (lane < kGemmRows)
-                __builtin_amdgcn_global_load_lds(
-                    plane + row, (lds_ptr_t)(trec + ((t & (kBf2RecSlots - 1)) * 3 + wave) * kGemmRows),
-                    4, 0, 0);
+                __builtin_amdgcn_global_load_lds(recs + row,
+                                                 (lds_ptr_t)(trec + (t & (kBf2RecSlots - 1)) * kGemmRows),
+                                                 16, 0, 0);
         }
     };
-
     // Keys of tile t's 8 rows of this lane (rows 8 (v / 4) + 4 h + v % 4
     // for v = 8 KP .. 8 KP + 7): this wave's sums plus the partner's, read
     // from LDS buffer t & 1.
@@ -597,43 +626,43 @@ __device__ __forceinline__ void bf2_segment(const uint16_t* __restrict__ hi_rows
         const int xo = ((t & 1) * kBf2Waves + ((wave + 4) & 7)) * 64 + lane;
         const f4v r0 = xa[xo];
         const f4v r1 = xb[xo];
-        const float* tr = trec + (t & (kBf2RecSlots - 1)) * 3 * kGemmRows;
+        const f4v* tr = trec + (t & (kBf2RecSlots - 1)) * kGemmRows;
 #pragma unroll
-        for (int g = 0; g < 2; ++g) {
-            const int m0 = 8 * (2 * KP + g) + 4 * h;
-            const f4v w4 = *reinterpret_cast<const f4v*>(tr + m0);
-            const f4v c4 = *reinterpret_cast<const f4v*>(tr + kGemmRows + m0);
-            f4v v4 = {};
-            if (METRIC != kMetricIP) v4 = *reinterpret_cast<const f4v*>(tr + 2 * kGemmRows + m0);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int i = 4 * g + j;
-                const float fv = keep[i] + (g == 0 ? r0[j] : r1[j]);
-                const float wv = w4[j], vc = c4[j], vn = v4[j];
-                float k;
-                if (METRIC == kMetricIP) {
-                    k = (-fv - sq * (wv * bc.c_ip + vc)) - ga.abs_slack;
-                } else if (METRIC == kMetricL2) {
-                    float dd = qn - 2.0f * fv + vn;
-                    dd = dd > 0.0f ? dd : 0.0f;
-                    k = (dd - ((qn + vn + 2.0f * (sq * wv)) * bc.c_l2 + sq * (2.0f * vc))) -
-                        ga.abs_slack;
-                } else {
-                    // A zero row has wv = vc = 0 and key 1 - eps (both paths
-                    // give exactly 1).
-                    k = (1.0f - fv * (rq * wv)) - (eps_all + vc);
-                    k = vn < vn_tiny ? -1.0f : k;
-                }
-                key[i] = k;
-            }
+        for (int i = 0; i < 8; ++i) {
+            const int v = 8 * KP + i;
+            const int m = 8 * (v >> 2) + 4 * h + (v & 3);
+            const float fv = keep[i] + (i < 4 ? r0[i] : r1[i - 4]);
+            key[i] = bf2_key<METRIC>(fv, qn, sq, rq, vn_tiny, tr[m], bc, eps_all, ga.abs_slack);
         }
     };
-    // The insertion path, only for a lane with a key at or below its
-    // threshold.
+    // The full launch appends keys at or below the query's bound to the
+    // query's region for this k half (its two lanes, h = 0 and 1, take
+    // consecutive slots by ballot; the threshold never changes); the
+    // sampled launch inserts into the lane's sorted list and lowers the
+    // lane's threshold as the list fills.
     auto offer = [&](const float (&key)[8], int t) {
         float mn = key[0];
 #pragma unroll
         for (int i = 1; i < 8; ++i) mn = fminf(mn, key[i]);
+        if (BOUNDED) {
+            if (__builtin_amdgcn_ballot_w64(mn <= thr) == 0) return;
+            const int64_t base = seg0 + (int64_t)t * kGemmRows;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const bool hit = key[i] <= thr;
+                const uint64_t m = __builtin_amdgcn_ballot_w64(hit);
+                if (m == 0) continue;
+                const uint32_t b0 = (uint32_t)(m >> col) & 1u, b1 = (uint32_t)(m >> (col + 32)) & 1u;
+                const uint32_t pos = cnt + (h ? b0 : 0u);
+                if (hit && pos < (uint32_t)(kBf2Cap / 2)) {
+                    const int v = 8 * KP + i;
+                    const int mrow = 8 * (v >> 2) + 4 * h + (v & 3);
+                    region[pos] = pack_slot(key[i], (uint32_t)(base + mrow));
+                }
+                cnt += b0 + b1;
+            }
+            return;
+        }
         if (mn <= thr) {
             const int64_t base = seg0 + (int64_t)t * kGemmRows;
 #pragma unroll
@@ -641,12 +670,8 @@ __device__ __forceinline__ void bf2_segment(const uint16_t* __restrict__ hi_rows
                 if (key[i] <= thr) {
                     const int v = 8 * KP + i;
                     const int m = 8 * (v >> 2) + 4 * h + (v & 3);
-                    const uint64_t slot = pack_slot(key[i], (uint32_t)(base + m));
-                    if (slot <= bound) {
-                        list_insert<C>(lst, slot);
-                        const uint64_t top = lst[C - 1] < bound ? lst[C - 1] : bound;
-                        thr = top == kEmptySlot ? thr : slot_key(top);
-                    }
+                    list_insert<C>(lst, pack_slot(key[i], (uint32_t)(base + m)));
+                    thr = lst[C - 1] == kEmptySlot ? thr : slot_key(lst[C - 1]);
                 }
             }
         }
@@ -671,7 +696,7 @@ __device__ __forceinline__ void bf2_segment(const uint16_t* __restrict__ hi_rows
         // tile t + 1 may still be in flight); the barrier publishes every
         // wave's loads and parts and frees slot (t - 1) % 3 for tile t + 2.
         if (t + 1 < ntiles) {
-            if (wave < 3) wait_vmcnt<G::LOADS + 1>();
+            if (wave == 0) wait_vmcnt<G::LOADS + 1>();
             else wait_vmcnt<G::LOADS>();
         } else {
             wait_vmcnt<0>();
@@ -685,7 +710,7 @@ __device__ __forceinline__ void bf2_segment(const uint16_t* __restrict__ hi_rows
         float key[8];
         keys(keep, t + 3, key);
         const uint8_t* xl = ring + cslot * G::SLOT_BYTES + KP * (16 * G::HALF_CHUNKS) + col * CPR * 16;
-        const int sw = col & SWZ;
+        const int sw = G::Swz::of(col);
         f16v acc = {};
 #pragma unroll
         for (int s = 0; s < NH; ++s) {
@@ -715,7 +740,21 @@ __device__ __forceinline__ void bf2_segment(const uint16_t* __restrict__ hi_rows
         }
         offer(key, ntiles - 1);
     }
-    if (qvalid) {
+    if (BOUNDED) {
+        // Pads the region with empty slots (lane h takes half of them); a
+        // region that filled up (it may have turned keys away) flags its
+        // query, which the streaming scan runs again.  The buffer's last
+        // slot is filled only then, so the merge's full-list cut stays
+        // empty.
+        if (qvalid) {
+#pragma unroll
+            for (int j = 0; j < kBf2Cap / 4; ++j) {
+                const uint32_t slot = (uint32_t)(h * (kBf2Cap / 4) + j);
+                if (slot >= cnt) region[slot] = kEmptySlot;
+            }
+            if (h == 0 && cnt >= (uint32_t)(kBf2Cap / 2)) atomicOr(ga.qflag + qid, 2u);
+        }
+    } else if (qvalid) {
         uint64_t* out = ga.lists + (((size_t)qid * ga.nseg + seg) * kBf2Lists + 2 * KP + h) * C;
 #pragma unroll
         for (int i = 0; i < C; ++i) out[i] = lst[i];
@@ -723,24 +762,21 @@ __device__ __forceinline__ void bf2_segment(const uint16_t* __restrict__ hi_rows
 }
 
 // grid: nseg * nqb blocks (1-D, XCD mapping as flat_gemm_f32); block 512.
-// hi_rows: the rows' bf16 high parts; wplane, cplane: per row w = sqrt(vn)
-// (1 / sqrt(vn) for cosine) and the remainder term without ||q|| (e' for
-// inner product and L2, e' / ||v|| for cosine); norms: vn; split_q: the
-// queries' split parts.
+// hi_rows: the rows' bf16 high parts; recs: per row {vn, w, c, 0} of the
+// metric (w = sqrt(vn), or 1 / sqrt(vn) for cosine; c the remainder term
+// without ||q||: e' for inner product and L2, e' / ||v|| for cosine);
+// split_q: the queries' split parts.
 template <int DIM, int METRIC, int C, bool BOUNDED>
 __global__ __launch_bounds__(512, 1) void flat_gemm_bf16x2(
-    const uint16_t* __restrict__ hi_rows, const float* __restrict__ wplane,
-    const float* __restrict__ cplane, const float* __restrict__ norms, int64_t n,
+    const uint16_t* __restrict__ hi_rows, const f4v* __restrict__ recs, int64_t n,
     const uint32_t* __restrict__ split_q, const float* __restrict__ queries, int64_t nq,
     BoundCoef bc, Bf2Args ga) {
     // The k half is uniform over a wave: a scalar branch.
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (wave < 4)
-        bf2_segment<DIM, METRIC, C, BOUNDED, 0>(hi_rows, wplane, cplane, norms, n, split_q, queries,
-                                               nq, bc, ga, wave);
+        bf2_segment<DIM, METRIC, C, BOUNDED, 0>(hi_rows, recs, n, split_q, queries, nq, bc, ga, wave);
     else
-        bf2_segment<DIM, METRIC, C, BOUNDED, 1>(hi_rows, wplane, cplane, norms, n, split_q, queries,
-                                               nq, bc, ga, wave);
+        bf2_segment<DIM, METRIC, C, BOUNDED, 1>(hi_rows, recs, n, split_q, queries, nq, bc, ga, wave);
 }
 
 // grid (1, nq), block 256: bound[q] = a slot with the key B and the largest
@@ -872,8 +908,9 @@ __global__ __launch_bounds__(256) void flat_lists_merge(
     if (qbound && qbound[q] != kEmptySlot) list_cut = fminf(list_cut, slot_key(qbound[q]));
     final_rescore_wide(qp, qn, rows, norms, n, dim, metric, q, top, ncand, kc, res,
                        reinterpret_cast<float*>(cand), fa, kProofFlat, kEmptySlot, list_cut);
-    // A query with values outside the split range has no valid keys here:
-    // the streaming scan runs it again.
+    // A query with values outside the split range has no valid keys here,
+    // and one whose candidate buffer filled up may miss rows: the streaming
+    // scan runs it again.
     if (tid == 0 && qbad && qbad[q]) fa.status[q] = 1;
 }
 
@@ -916,7 +953,11 @@ bool plan_gemm(int64_t n, int dim, int64_t nq, int kc, GemmPlan* out) {
     p.s_nseg = (int)std::min<int64_t>(nseg, 64);
     const int64_t srps = (n + p.s_nseg - 1) / p.s_nseg;
     p.s_rows_per_seg = (srps + kGemmRows - 1) / kGemmRows * kGemmRows;
-    int64_t srows = (n / 32 / p.s_nseg + kGemmRows - 1) / kGemmRows * kGemmRows;
+    static const int64_t sdiv = [] {
+        const char* e = std::getenv("MANS_BF2_SAMPLE");
+        return e ? std::max<int64_t>(1, std::atoll(e)) : (int64_t)32;
+    }();
+    int64_t srows = (n / sdiv / p.s_nseg + kGemmRows - 1) / kGemmRows * kGemmRows;
     srows = std::max<int64_t>(srows, kGemmRows);
     p.s_seg_rows = std::min(srows, p.s_rows_per_seg);
     *out = p;
@@ -941,65 +982,64 @@ static double bf2_unit_roundoff(int dim) {
 
 struct Bf2Inputs {
     const uint16_t* hi_rows;
-    const float* wplane;
-    const float* cplane;
-    const float* norms;
+    const f4v* recs;
     int64_t n;
     const uint32_t* split_q;
     const float* queries;
     int64_t nq;
 };
 
-template <int DIM, int C, bool BOUNDED>
-static void launch_bf2_dim_c(const GemmPlan& p, const Bf2Inputs& in, int metric, const Bf2Args& ga,
-                             hipStream_t s) {
+template <int DIM, int C>
+static void launch_bf2_dim_c(const GemmPlan& p, bool sampled, const Bf2Inputs& in, int metric,
+                             const Bf2Args& ga, hipStream_t s) {
     const BoundCoef bc = make_bounds(DIM, bf2_unit_roundoff(DIM));
     const dim3 grid((unsigned)(ga.nseg * p.nqb));
-    const size_t shmem = bf2_lds_bytes<DIM>();
+    const dim3 block(64 * kBf2Waves);
+    const size_t shm = bf2_lds_bytes<DIM>();
     static bool attr = [] {
-        (void)hipFuncSetAttribute((const void*)flat_gemm_bf16x2<DIM, kMetricCosine, C, BOUNDED>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)bf2_lds_bytes<DIM>());
-        (void)hipFuncSetAttribute((const void*)flat_gemm_bf16x2<DIM, kMetricL2, C, BOUNDED>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)bf2_lds_bytes<DIM>());
-        (void)hipFuncSetAttribute((const void*)flat_gemm_bf16x2<DIM, kMetricIP, C, BOUNDED>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)bf2_lds_bytes<DIM>());
+        const int a = (int)bf2_lds_bytes<DIM>();
+        (void)hipFuncSetAttribute((const void*)flat_gemm_bf16x2<DIM, kMetricCosine, C, false>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, a);
+        (void)hipFuncSetAttribute((const void*)flat_gemm_bf16x2<DIM, kMetricL2, C, false>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, a);
+        (void)hipFuncSetAttribute((const void*)flat_gemm_bf16x2<DIM, kMetricIP, C, false>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, a);
+        (void)hipFuncSetAttribute((const void*)flat_gemm_bf16x2<DIM, kMetricCosine, C, true>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, a);
+        (void)hipFuncSetAttribute((const void*)flat_gemm_bf16x2<DIM, kMetricL2, C, true>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, a);
+        (void)hipFuncSetAttribute((const void*)flat_gemm_bf16x2<DIM, kMetricIP, C, true>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, a);
         return true;
     }();
     (void)attr;
-    const dim3 block(64 * kBf2Waves);
-    switch (metric) {
-    case kMetricCosine:
-        hipLaunchKernelGGL((flat_gemm_bf16x2<DIM, kMetricCosine, C, BOUNDED>), grid, block, shmem,
-                           s, in.hi_rows, in.wplane, in.cplane, in.norms, in.n, in.split_q, in.queries, in.nq, bc, ga);
-        break;
-    case kMetricL2:
-        hipLaunchKernelGGL((flat_gemm_bf16x2<DIM, kMetricL2, C, BOUNDED>), grid, block, shmem, s,
-                           in.hi_rows, in.wplane, in.cplane, in.norms, in.n, in.split_q, in.queries, in.nq, bc, ga);
-        break;
-    default:
-        hipLaunchKernelGGL((flat_gemm_bf16x2<DIM, kMetricIP, C, BOUNDED>), grid, block, shmem, s,
-                           in.hi_rows, in.wplane, in.cplane, in.norms, in.n, in.split_q, in.queries, in.nq, bc, ga);
-        break;
-    }
-}
-
-template <int DIM>
-static void launch_bf2_dim(const GemmPlan& p, bool bounded, const Bf2Inputs& in, int metric,
-                           const Bf2Args& ga, hipStream_t s) {
-    if (gemm_list_len(p.kc) == 4) {
-        if (bounded) launch_bf2_dim_c<DIM, 4, true>(p, in, metric, ga, s);
-        else launch_bf2_dim_c<DIM, 4, false>(p, in, metric, ga, s);
+#define MANS_BF2_LAUNCH(M, B)                                                                      \
+    hipLaunchKernelGGL((flat_gemm_bf16x2<DIM, M, C, B>), grid, block, shm, s, in.hi_rows, in.recs, \
+                       in.n, in.split_q, in.queries, in.nq, bc, ga)
+    if (sampled) {
+        switch (metric) {
+        case kMetricCosine: MANS_BF2_LAUNCH(kMetricCosine, false); break;
+        case kMetricL2: MANS_BF2_LAUNCH(kMetricL2, false); break;
+        default: MANS_BF2_LAUNCH(kMetricIP, false); break;
+        }
     } else {
-        if (bounded) launch_bf2_dim_c<DIM, 8, true>(p, in, metric, ga, s);
-        else launch_bf2_dim_c<DIM, 8, false>(p, in, metric, ga, s);
+        switch (metric) {
+        case kMetricCosine: MANS_BF2_LAUNCH(kMetricCosine, true); break;
+        case kMetricL2: MANS_BF2_LAUNCH(kMetricL2, true); break;
+        default: MANS_BF2_LAUNCH(kMetricIP, true); break;
+        }
     }
+#undef MANS_BF2_LAUNCH
 }
 
 hipError_t launch_flat_bf2(const GemmPlan& p, bool sampled, const uint16_t* hi_rows,
-                           const float* recs, const float* norms, int64_t n, int dim,
-                           const uint32_t* split_q,
+                           const float* recs, int64_t n, int dim, const uint32_t* split_q,
                            const float* queries, int64_t nq, int metric, const uint64_t* qbound,
-                           uint64_t* lists, hipStream_t s) {
+                           uint64_t* lists, uint32_t* qflag, hipStream_t s) {
+    // The split path keeps kGemmMaxKc candidates: 8-slot lane lists in the
+    // sampled launch, kBf2Cap-slot buffers (a half per k half) in the full
+    // one.
+    if (gemm_list_len(p.kc) * kBf2Lists != kBf2Cap) return hipErrorInvalidValue;
     Bf2Args ga;
     ga.nseg = sampled ? p.s_nseg : p.nseg;
     ga.nqb = p.nqb;
@@ -1010,18 +1050,18 @@ hipError_t launch_flat_bf2(const GemmPlan& p, bool sampled, const uint16_t* hi_r
     ga.abs_slack = (float)(12.0 * dim * 1.1754943508222875e-38);
     ga.qbound = qbound;
     ga.lists = lists;
-    const bool bounded = !sampled;
-    // The planes of the metric: [4][n] = cosine w, cosine c, L2 and inner
-    // product w, L2 and inner product c.
-    const float* wp = recs + (metric == kMetricCosine ? 0 : 2 * n);
-    const Bf2Inputs in{hi_rows, wp, wp + n, norms, n, split_q, queries, nq};
+    ga.qflag = qflag;
+    // The records of the metric: [n] for cosine, then [n] for L2 and inner
+    // product.
+    const f4v* r4 = reinterpret_cast<const f4v*>(recs) + (metric == kMetricCosine ? 0 : n);
+    const Bf2Inputs in{hi_rows, r4, n, split_q, queries, nq};
     switch (dim) {
-    case 64: launch_bf2_dim<64>(p, bounded, in, metric, ga, s); break;
-    case 96: launch_bf2_dim<96>(p, bounded, in, metric, ga, s); break;
-    case 128: launch_bf2_dim<128>(p, bounded, in, metric, ga, s); break;
-    case 192: launch_bf2_dim<192>(p, bounded, in, metric, ga, s); break;
-    case 256: launch_bf2_dim<256>(p, bounded, in, metric, ga, s); break;
-    case 384: launch_bf2_dim<384>(p, bounded, in, metric, ga, s); break;
+    case 64: launch_bf2_dim_c<64, 8>(p, sampled, in, metric, ga, s); break;
+    case 96: launch_bf2_dim_c<96, 8>(p, sampled, in, metric, ga, s); break;
+    case 128: launch_bf2_dim_c<128, 8>(p, sampled, in, metric, ga, s); break;
+    case 192: launch_bf2_dim_c<192, 8>(p, sampled, in, metric, ga, s); break;
+    case 256: launch_bf2_dim_c<256, 8>(p, sampled, in, metric, ga, s); break;
+    case 384: launch_bf2_dim_c<384, 8>(p, sampled, in, metric, ga, s); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -1092,9 +1132,13 @@ static void launch_lists_merge(const GemmPlan& p, const float* rows, const float
     const size_t stage = sizeof(float) * 2 * 64 * kWideStride;
     const size_t slots = total <= kKthLdsSlots ? sizeof(uint64_t) * (size_t)total : 0;
     const size_t shmem = sizeof(uint64_t) * 512 + std::max(stage, slots);
+    // The split-bf16 path (qbound set) leaves one candidate buffer per
+    // segment; the fp32 contraction lps sorted lane lists per segment.
+    const int nlists = qbound ? p.nseg : p.lps * p.nseg;
+    const int list_len = (int)(total / nlists);
     hipLaunchKernelGGL(flat_lists_merge<NCH>, dim3(1, (unsigned)nq), dim3(256), shmem, s, rows,
-                       norms, n, dim, queries, metric, p.kc, p.cap, p.lps * p.nseg,
-                       gemm_list_len(p.kc), lists, qbound, qbad, fa);
+                       norms, n, dim, queries, metric, p.kc, p.cap, nlists, list_len, lists,
+                       qbound, qbad, fa);
 }
 
 hipError_t launch_flat_gemm(const GemmPlan& p, const float* rows, const float* norms, int64_t n,

@@ -75,19 +75,19 @@ hipError_t launch_flat_gemm_merge(const GemmPlan& p, const float* rows, const fl
 // (other than 0).
 hipError_t launch_split_queries(const float* src, int64_t count, int dim, uint32_t* dst,
                                 uint32_t* bad, hipStream_t s);
-// Rows: hi gets the bf16 high parts ([count][dim]), recs four per-row
-// planes ([4][count] floats: the cosine keys' w and c, then those of L2 and
-// inner product) from the rows and their squared norms; bad[0] is or-ed
-// with 1 for a value outside the range.
+// Rows: hi gets the bf16 high parts ([count][dim]), recs the per-row key
+// records ([2][count] float4s: cosine, then L2 and inner product) from the
+// rows and their squared norms; bad[0] is or-ed with 1 for a value outside
+// the range.
 hipError_t launch_split_rows(const float* src, const float* norms, int64_t count, int dim,
                              uint16_t* hi, float* recs, uint32_t* bad, hipStream_t s);
-// sampled: the bounding launch (no bounds); otherwise the full launch with
-// the per-query bounds qbound.  Writes the lane lists.
+// sampled: the bounding launch (no bounds, sorted lane lists); otherwise the
+// full launch with the per-query bounds qbound (candidate buffers; a query
+// whose buffer fills up gets bit 2 in qflag).
 hipError_t launch_flat_bf2(const GemmPlan& p, bool sampled, const uint16_t* hi_rows,
-                           const float* recs, const float* norms, int64_t n, int dim,
-                           const uint32_t* split_q,
+                           const float* recs, int64_t n, int dim, const uint32_t* split_q,
                            const float* queries, int64_t nq, int metric, const uint64_t* qbound,
-                           uint64_t* lists, hipStream_t s);
+                           uint64_t* lists, uint32_t* qflag, hipStream_t s);
 // bound[q]: from the sampled lists of query q, a slot whose key is the
 // largest exact distance among the k rows with the smallest keys.
 hipError_t launch_bf2_bounds(const GemmPlan& p, int64_t nq, int k, const uint64_t* lists,

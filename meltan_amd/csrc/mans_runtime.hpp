@@ -98,7 +98,7 @@ struct mans_corpus {
     // int8 planes (Int8CodeCache.swift:22-108), built on first use.
     bool int8_valid = false;
     mans::DevBuf i8_codes, i8_u, i8_w, i8_normsq, i8_invsqrt;
-    // The rows' bf16 high parts ([n][dim]) and key planes ([4][n] floats)
+    // The rows' bf16 high parts ([n][dim]) and key records ([2][n] float4s)
     // for the batched split-bf16 contraction, built on first use; bf_ok:
     // every value is in the split range.
     bool bf_valid = false;
