@@ -415,7 +415,7 @@ constexpr int kBf2Waves = 8;
 constexpr int kBf2Slots = 3;     // row tile ring: tile t + 2 loads while tile t is used
 constexpr int kBf2RecSlots = 4;  // row record ring
 constexpr int kBf2Lists = 4;     // sampled launch: lane lists per query and segment
-constexpr int kBf2Cap = 32;      // full launch: candidate slots per query and segment
+constexpr int kBf2Cap = 64;      // full launch: candidate slots per query and segment
 // The full launch's 32 x 32 sums of a query group, query-major: query q's
 // 32 rows start at q * kBf2DotStride + (q / 16) * 32 floats (16-byte
 // aligned; the key waves' two query halves fall on different banks).
@@ -948,16 +948,12 @@ bool plan_gemm(int64_t n, int dim, int64_t nq, int kc, GemmPlan* out) {
     int64_t rps = (n + nseg - 1) / nseg;
     p.rows_per_seg = (rps + kGemmRows - 1) / kGemmRows * kGemmRows;
     p.nseg = (int)nseg;
-    // Bounding launch of the split-bf16 contraction: up to 64 segments
+    // Bounding launch of the split-bf16 contraction: up to 32 segments
     // spread over the rows, about a thirty-second of the rows in all.
-    p.s_nseg = (int)std::min<int64_t>(nseg, 64);
+    p.s_nseg = (int)std::min<int64_t>(nseg, 32);
     const int64_t srps = (n + p.s_nseg - 1) / p.s_nseg;
     p.s_rows_per_seg = (srps + kGemmRows - 1) / kGemmRows * kGemmRows;
-    static const int64_t sdiv = [] {
-        const char* e = std::getenv("MANS_BF2_SAMPLE");
-        return e ? std::max<int64_t>(1, std::atoll(e)) : (int64_t)32;
-    }();
-    int64_t srows = (n / sdiv / p.s_nseg + kGemmRows - 1) / kGemmRows * kGemmRows;
+    int64_t srows = (n / 32 / p.s_nseg + kGemmRows - 1) / kGemmRows * kGemmRows;
     srows = std::max<int64_t>(srows, kGemmRows);
     p.s_seg_rows = std::min(srows, p.s_rows_per_seg);
     *out = p;
@@ -965,7 +961,10 @@ bool plan_gemm(int64_t n, int dim, int64_t nq, int kc, GemmPlan* out) {
 }
 
 size_t gemm_lists_bytes(const GemmPlan& p, int64_t nq) {
-    return (size_t)nq * (size_t)p.nseg * p.lps * gemm_list_len(p.kc) * sizeof(uint64_t);
+    // The split-bf16 path (lps 4): the full launch's candidate buffers,
+    // which also hold the sampled launch's lane lists (s_nseg <= nseg).
+    const size_t per = p.lps == 4 ? (size_t)kBf2Cap : (size_t)p.lps * gemm_list_len(p.kc);
+    return (size_t)nq * (size_t)p.nseg * per * sizeof(uint64_t);
 }
 
 // Unit roundoff for make_bounds that covers the split-bf16 dot error
@@ -1039,7 +1038,7 @@ hipError_t launch_flat_bf2(const GemmPlan& p, bool sampled, const uint16_t* hi_r
     // The split path keeps kGemmMaxKc candidates: 8-slot lane lists in the
     // sampled launch, kBf2Cap-slot buffers (a half per k half) in the full
     // one.
-    if (gemm_list_len(p.kc) * kBf2Lists != kBf2Cap) return hipErrorInvalidValue;
+    if (gemm_list_len(p.kc) * kBf2Lists > kBf2Cap) return hipErrorInvalidValue;
     Bf2Args ga;
     ga.nseg = sampled ? p.s_nseg : p.nseg;
     ga.nqb = p.nqb;
@@ -1127,15 +1126,15 @@ static void launch_lists_merge(const GemmPlan& p, const float* rows, const float
                                int dim, const float* queries, int64_t nq, int metric,
                                const uint64_t* lists, const uint64_t* qbound,
                                const uint32_t* qbad, const FlatArgs& fa, hipStream_t s) {
-    const int64_t total = (int64_t)p.lps * p.nseg * gemm_list_len(p.kc);
+    // The split-bf16 path (qbound set) leaves one candidate buffer per
+    // segment; the fp32 contraction lps sorted lane lists per segment.
+    const int nlists = qbound ? p.nseg : p.lps * p.nseg;
+    const int list_len = qbound ? kBf2Cap : gemm_list_len(p.kc);
+    const int64_t total = (int64_t)nlists * list_len;
     static_assert(kGemmMaxKc <= 64, "the merge's rescore stages one group of 64 rows");
     const size_t stage = sizeof(float) * 2 * 64 * kWideStride;
     const size_t slots = total <= kKthLdsSlots ? sizeof(uint64_t) * (size_t)total : 0;
     const size_t shmem = sizeof(uint64_t) * 512 + std::max(stage, slots);
-    // The split-bf16 path (qbound set) leaves one candidate buffer per
-    // segment; the fp32 contraction lps sorted lane lists per segment.
-    const int nlists = qbound ? p.nseg : p.lps * p.nseg;
-    const int list_len = (int)(total / nlists);
     hipLaunchKernelGGL(flat_lists_merge<NCH>, dim3(1, (unsigned)nq), dim3(256), shmem, s, rows,
                        norms, n, dim, queries, metric, p.kc, p.cap, nlists, list_len, lists,
                        qbound, qbad, fa);
