@@ -415,6 +415,7 @@ constexpr int kBf2Waves = 8;
 constexpr int kBf2Slots = 3;     // row tile ring: tile t + 2 loads while tile t is used
 constexpr int kBf2RecSlots = 4;  // row record ring
 constexpr int kBf2Lists = 4;     // sampled launch: lane lists per query and segment
+constexpr int kBf2ListLen = 4;   // sampled launch: slots per lane list
 constexpr int kBf2Cap = 64;      // full launch: candidate slots per query and segment
 // The full launch's 32 x 32 sums of a query group, query-major: query q's
 // 32 rows start at q * kBf2DotStride + (q / 16) * 32 floats (16-byte
@@ -478,7 +479,7 @@ struct Bf2Args {
     int64_t seg_rows;         // rows scanned from each segment's start
     float abs_slack;
     const uint64_t* qbound;   // full launch: per query
-    // Sampled launch: lane lists [nq][nseg][kBf2Lists][C].  Full launch:
+    // Sampled launch: lane lists [nq][nseg][kBf2Lists][kBf2ListLen].  Full launch:
     // candidate buffers [nq][nseg][kBf2Cap], unsorted, padded with
     // kEmptySlot; a buffer that fills up sets bit 2 of qflag[query].
     uint64_t* lists;
@@ -876,18 +877,27 @@ __global__ __launch_bounds__(256) void flat_lists_merge(
     }
     const uint64_t full_cut = block_reduce_u64<false>(mine);
     const bool in_lds = total <= kKthLdsSlots;
-    if (in_lds)
-        for (int64_t i = tid; i < total; i += blockDim.x) cand[i] = lq[i];
     __shared__ uint32_t hist[256];
-    __shared__ int ntop;
-    if (tid == 0) ntop = 0;
+    __shared__ int ntop, nkept;
+    if (tid == 0) {
+        ntop = 0;
+        nkept = 0;
+    }
     __syncthreads();
+    // The non-empty slots, compacted into LDS when they fit (in any order).
+    if (in_lds)
+        for (int64_t i = tid; i < total; i += blockDim.x) {
+            const uint64_t s = lq[i];
+            if (s != kEmptySlot) cand[atomicAdd(&nkept, 1)] = s;
+        }
+    __syncthreads();
+    const int64_t nslots = in_lds ? (int64_t)nkept : total;
     // The kc smallest slots (empty slots are the largest values and are
     // never taken).
     auto get = [&](int64_t i) { return in_lds ? cand[i] : lq[i]; };
     uint64_t kth;
-    const uint64_t sel = block_radix_cut(get, total, kc, hist, &kth);
-    for (int64_t i = tid; i < total; i += blockDim.x) {
+    const uint64_t sel = block_radix_cut(get, nslots, kc, hist, &kth);
+    for (int64_t i = tid; i < nslots; i += blockDim.x) {
         const uint64_t s = get(i);
         if (s != kEmptySlot && s <= sel) {
             const int p = atomicAdd(&ntop, 1);
@@ -1035,10 +1045,10 @@ hipError_t launch_flat_bf2(const GemmPlan& p, bool sampled, const uint16_t* hi_r
                            const float* recs, int64_t n, int dim, const uint32_t* split_q,
                            const float* queries, int64_t nq, int metric, const uint64_t* qbound,
                            uint64_t* lists, uint32_t* qflag, hipStream_t s) {
-    // The split path keeps kGemmMaxKc candidates: 8-slot lane lists in the
-    // sampled launch, kBf2Cap-slot buffers (a half per k half) in the full
-    // one.
-    if (gemm_list_len(p.kc) * kBf2Lists > kBf2Cap) return hipErrorInvalidValue;
+    // The sampled launch keeps kBf2ListLen-slot lane lists (its bound needs
+    // only the k <= 32 best rows); the full one kBf2Cap-slot candidate
+    // buffers (a half per k half), of which the merge keeps kGemmMaxKc.
+    static_assert(kBf2Lists * kBf2ListLen <= kBf2Cap, "sampled lists fit the buffers");
     Bf2Args ga;
     ga.nseg = sampled ? p.s_nseg : p.nseg;
     ga.nqb = p.nqb;
@@ -1054,13 +1064,14 @@ hipError_t launch_flat_bf2(const GemmPlan& p, bool sampled, const uint16_t* hi_r
     // product.
     const f4v* r4 = reinterpret_cast<const f4v*>(recs) + (metric == kMetricCosine ? 0 : n);
     const Bf2Inputs in{hi_rows, r4, n, split_q, queries, nq};
+    constexpr int C = kBf2ListLen;
     switch (dim) {
-    case 64: launch_bf2_dim_c<64, 8>(p, sampled, in, metric, ga, s); break;
-    case 96: launch_bf2_dim_c<96, 8>(p, sampled, in, metric, ga, s); break;
-    case 128: launch_bf2_dim_c<128, 8>(p, sampled, in, metric, ga, s); break;
-    case 192: launch_bf2_dim_c<192, 8>(p, sampled, in, metric, ga, s); break;
-    case 256: launch_bf2_dim_c<256, 8>(p, sampled, in, metric, ga, s); break;
-    case 384: launch_bf2_dim_c<384, 8>(p, sampled, in, metric, ga, s); break;
+    case 64: launch_bf2_dim_c<64, C>(p, sampled, in, metric, ga, s); break;
+    case 96: launch_bf2_dim_c<96, C>(p, sampled, in, metric, ga, s); break;
+    case 128: launch_bf2_dim_c<128, C>(p, sampled, in, metric, ga, s); break;
+    case 192: launch_bf2_dim_c<192, C>(p, sampled, in, metric, ga, s); break;
+    case 256: launch_bf2_dim_c<256, C>(p, sampled, in, metric, ga, s); break;
+    case 384: launch_bf2_dim_c<384, C>(p, sampled, in, metric, ga, s); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -1069,7 +1080,7 @@ hipError_t launch_flat_bf2(const GemmPlan& p, bool sampled, const uint16_t* hi_r
 hipError_t launch_bf2_bounds(const GemmPlan& p, int64_t nq, int k, const uint64_t* lists,
                              const float* rows, const float* norms, int dim, const float* queries,
                              int metric, uint64_t* bound, hipStream_t s) {
-    const int64_t per_query = (int64_t)p.s_nseg * kBf2Lists * gemm_list_len(p.kc);
+    const int64_t per_query = (int64_t)p.s_nseg * kBf2Lists * kBf2ListLen;
     const size_t shmem = per_query <= kKthLdsSlots ? sizeof(uint64_t) * (size_t)per_query : 0;
     const dim3 grid(1, (unsigned)nq);
 #define MANS_BOUND_CASE(N)                                                                       \
