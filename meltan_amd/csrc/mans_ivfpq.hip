@@ -197,33 +197,6 @@ __device__ inline int sorted_list_insert_run(const float* in_score, uint32_t tag
     return count;
 }
 
-// simd_distance with b read at stride bstride (centroids stored
-// dimension-major, so consecutive lanes read consecutive floats); the same
-// operations in the same order.
-__device__ __forceinline__ float simd_distance_strided(const float* a, const float* b, int d,
-                                                       int64_t bstride, int metric) {
-    if (metric == kMetricL2) {
-        float s = 0.0f;
-        for (int i = 0; i < d; ++i) {
-            const float t = a[i] - b[i * bstride];
-            s += t * t;
-        }
-        return s;
-    }
-    if (metric == kMetricIP) {
-        float dot = 0.0f;
-        for (int i = 0; i < d; ++i) dot += a[i] * b[i * bstride];
-        return -dot;
-    }
-    if (d <= 0) return 1.0f;
-    float dot = 0.0f, na = 0.0f, nb = 0.0f;
-    for (int i = 0; i < d; ++i) dot += a[i] * b[i * bstride];
-    for (int i = 0; i < d; ++i) na += a[i] * a[i];
-    for (int i = 0; i < d; ++i) nb += b[i * bstride] * b[i * bstride];
-    const float denom = sqrtf(na) * sqrtf(nb);
-    return denom < 1e-10f ? 1.0f : 1.0f - dot / denom;
-}
-
 // dst[d][c] = src[c][d] for a rows x cols matrix.
 __global__ void transpose_kernel(const float* __restrict__ src, int64_t rows, int cols,
                                  float* __restrict__ dst) {
@@ -234,31 +207,92 @@ __global__ void transpose_kernel(const float* __restrict__ src, int64_t rows, in
     dst[(int64_t)c * rows + r] = src[i];
 }
 
+// Distances from kPqDistQ queries to every centroid (SIMDDistance.distance,
+// SIMDDistance.swift:17-80, as sequential sums: each (query, centroid) pair
+// in the same operations and order as simd_distance).  grid
+// (ceil(nlist / 256), ceil(nq / kPqDistQ)), block 256: thread c takes
+// centroid c for the block's queries, so each centroid value read from
+// coarse_t ([dim][nlist]) serves all of them.  dist: [nq][nlist].
+constexpr int kPqDistQ = 16;
+
+template <int METRIC>
+__global__ __launch_bounds__(256) void pq_coarse_dist(const float* __restrict__ queries, int64_t nq,
+                                                      int dim, const float* __restrict__ coarse_t,
+                                                      int nlist, float* __restrict__ dist) {
+    extern __shared__ float qs[];  // [kPqDistQ][dim], then the queries' sums of squares
+    float* qsq = qs + kPqDistQ * dim;
+    const int tid = threadIdx.x;
+    const int64_t q0 = (int64_t)blockIdx.y * kPqDistQ;
+    for (int i = tid; i < kPqDistQ * dim; i += blockDim.x) {
+        const int j = i / dim;
+        qs[i] = q0 + j < nq ? queries[(q0 + j) * dim + (i - j * dim)] : 0.0f;
+    }
+    __syncthreads();
+    if (METRIC == kMetricCosine && tid < kPqDistQ) {
+        float na = 0.0f;
+        for (int i = 0; i < dim; ++i) na += qs[tid * dim + i] * qs[tid * dim + i];
+        qsq[tid] = na;
+    }
+    __syncthreads();
+    const int c = blockIdx.x * blockDim.x + tid;
+    if (c >= nlist) return;
+    float acc[kPqDistQ];
+#pragma unroll
+    for (int j = 0; j < kPqDistQ; ++j) acc[j] = 0.0f;
+    float nb = 0.0f;
+    for (int i = 0; i < dim; ++i) {
+        const float b = coarse_t[(int64_t)i * nlist + c];
+#pragma unroll
+        for (int j = 0; j < kPqDistQ; ++j) {
+            const float a = qs[j * dim + i];
+            if (METRIC == kMetricL2) {
+                const float t = a - b;
+                acc[j] += t * t;
+            } else {
+                acc[j] += a * b;
+            }
+        }
+        if (METRIC == kMetricCosine) nb += b * b;
+    }
+#pragma unroll
+    for (int j = 0; j < kPqDistQ; ++j) {
+        if (q0 + j >= nq) break;
+        float d;
+        if (METRIC == kMetricL2) {
+            d = acc[j];
+        } else if (METRIC == kMetricIP) {
+            d = -acc[j];
+        } else if (dim <= 0) {
+            d = 1.0f;
+        } else {
+            const float denom = sqrtf(qsq[j]) * sqrtf(nb);
+            d = denom < 1e-10f ? 1.0f : 1.0f - acc[j] / denom;
+        }
+        dist[(q0 + j) * nlist + c] = d;
+    }
+}
+
 // Probe selection, one block per query (selectClosestCentroids,
-// IVFPQIndex.swift:484-512): the sequential distance to every centroid, the
-// np + 64 smallest by (distance, index), then the BoundedSortedList(np)
-// order over those at or below the np-th distance.  When more centroids tie
-// at the np-th distance than those kept (a zero query, duplicate
-// centroids), the list is replayed over every centroid in index order
-// instead.  dynamic LDS: 4 * cap slots + dim floats; cap >= 2 np + 128.
-__global__ __launch_bounds__(256) void pq_probes(const float* __restrict__ queries, int dim,
-                                                 const float* __restrict__ coarse_t, int nlist,
-                                                 int metric, int np, int kc, int cap,
+// IVFPQIndex.swift:484-512): from the query's distances to every centroid
+// (pq_coarse_dist), the np + 64 smallest by (distance, index), then the
+// BoundedSortedList(np) order over those at or below the np-th distance.
+// When more centroids tie at the np-th distance than those kept (a zero
+// query, duplicate centroids), the list is replayed over every centroid in
+// index order instead.  dynamic LDS: 4 * cap slots; cap >= 2 np + 128.
+__global__ __launch_bounds__(256) void pq_probes(const float* __restrict__ dists, int nlist,
+                                                 int np, int kc, int cap,
                                                  uint32_t* __restrict__ probes) {
     extern __shared__ uint64_t lds[];
-    float* qs = reinterpret_cast<float*>(lds + 4 * cap);
     __shared__ int s_cnt, s_over, s_len;
     const int tid = threadIdx.x, wave = tid >> 6;
     const int64_t q = blockIdx.x;
-    for (int d = tid; d < dim; d += blockDim.x) qs[d] = queries[q * dim + d];
-    __syncthreads();
+    const float* qd = dists + q * nlist;
     WaveTopK sel;
     sel.init(lds + wave * cap, cap, kc);
     for (int base = 0; base < nlist; base += blockDim.x) {
         const int c = base + tid;
         const bool v = c < nlist;
-        const float dist = v ? simd_distance_strided(qs, coarse_t + c, dim, nlist, metric) : 0.0f;
-        sel.offer(v, dist, (uint32_t)c);
+        sel.offer(v, v ? qd[c] : 0.0f, (uint32_t)c);
     }
     sel.finish();
     __syncthreads();
@@ -290,7 +324,7 @@ __global__ __launch_bounds__(256) void pq_probes(const float* __restrict__ queri
         for (int base = 0; base < nlist; base += 256) {
             const int c = base + tid;
             __syncthreads();
-            if (c < nlist) chunk[tid] = simd_distance_strided(qs, coarse_t + c, dim, nlist, metric);
+            if (c < nlist) chunk[tid] = qd[c];
             __syncthreads();
             if (tid == 0) {
                 const int m = nlist - base < 256 ? nlist - base : 256;
@@ -326,6 +360,8 @@ __global__ __launch_bounds__(256) void pq_probes(const float* __restrict__ queri
         for (int i = 0; i < np; ++i) probes[q * np + i] = i < cnt ? lt[i] : lt[0];
     }
 }
+
+constexpr int kPqMaxM = 64;      // LUT of m x 256 floats in LDS
 
 struct PqArgs {
     const uint8_t* codes;      // [n][m], packed list by list
@@ -439,7 +475,11 @@ __device__ __forceinline__ void pq_finish(const PqArgs& pa, const int64_t* seg, 
 
 // 1-D grid over work items; block 256; dynamic LDS: 4 * cap slots, then
 // m * 256 + dim floats (LUT, residual).  Slots are (score, arrival index).
-template <int NCH>
+// MR > 0: two-dimensional subvectors with m <= MR a multiple of 16 (the
+// codebook entries of this thread stay in registers, codes load as 16-byte
+// words); MR = 0: any shape.  CAPT > 0: the wave lists' capacity is CAPT
+// (their sorts compiled for that size).
+template <int NCH, int MR, int CAPT>
 __global__ __launch_bounds__(256) void ivfpq_scan(PqArgs pa, const float* __restrict__ queries,
                                                   const uint32_t* __restrict__ qidx, int kc, int cap,
                                                   FlatArgs fa) {
@@ -463,8 +503,23 @@ __global__ __launch_bounds__(256) void ivfpq_scan(PqArgs pa, const float* __rest
 
     const int64_t lo = (int64_t)j * pa.chunk;
     const int64_t hi = lo + pa.chunk < total ? lo + pa.chunk : total;
-    WaveTopK sel;
+    WaveTopKT<CAPT> sel;
     sel.init(lds + wave * cap, cap, kc);
+    // MR > 0: this thread's codebook entries (code tid of every subspace)
+    // stay in registers for all probes.
+    constexpr int NB = MR > 0 ? MR : 1;
+    constexpr int NC = MR > 0 ? MR / 16 : 4;  // 16-byte code words per row
+    float2 bk[NB];
+    if (MR > 0) {
+        const float2* b2 = reinterpret_cast<const float2*>(pa.books);
+#pragma unroll
+        for (int u = 0; u < NB; ++u) bk[u] = u < pa.m ? b2[u * 256 + tid] : make_float2(0.0f, 0.0f);
+    }
+    // Codes of a row as 16-byte loads when m is a multiple of 16 (rows
+    // then start 16-byte aligned), two 256-row batches ahead of their
+    // scores (the first two while the LUT is built).  The score adds the m
+    // entries in code order (IVFPQIndex.swift:418-452) either way.
+    const int m16 = (pa.m & 15) == 0 && pa.m <= 16 * NC ? pa.m >> 4 : 0;
     for (int p = 0; p < pa.np; ++p) {
         const int64_t pre = seg[2 * p + 1];
         if (pre >= hi) break;
@@ -478,35 +533,39 @@ __global__ __launch_bounds__(256) void ivfpq_scan(PqArgs pa, const float* __rest
         for (int d = tid; d < pa.dim; d += 256) qres[d] = qp[d] - cen[d];
         __syncthreads();
         const uint32_t* crow = reinterpret_cast<const uint32_t*>(pa.codes + (seg[2 * p] + a) * pa.m);
-        // Codes of a row as 16-byte loads when m is a multiple of 16 (rows
-        // then start 16-byte aligned); the next 256 rows' codes load while
-        // the current ones are scored, and the first ones while the LUT is
-        // built.  The score adds the m entries in code order
-        // (IVFPQIndex.swift:418-452) either way.
-        const int m16 = (pa.m & 15) == 0 && pa.m <= 64 ? pa.m >> 4 : 0;
         const int64_t nrow = b - a;
-        auto load_codes = [&](int64_t r, i4v (&c4)[4]) {
+        auto load_codes = [&](int64_t r, i4v (&c4)[NC]) {
             const uint32_t* cw = crow + (r < nrow ? r : 0) * mw;
 #pragma unroll
-            for (int c = 0; c < 4; ++c)
+            for (int c = 0; c < NC; ++c)
                 c4[c] = c < m16 ? reinterpret_cast<const i4v*>(cw)[c] : i4v{0, 0, 0, 0};
         };
-        i4v cur[4];
-        if (m16 > 0) load_codes(tid, cur);
-        pq_build_lut(pa, qres, lut);
+        i4v ca[NC], cb[NC], cc[NC];
+        if (m16 > 0) {
+            load_codes(tid, ca);
+            load_codes(256 + tid, cb);
+        }
+        if (MR > 0) {
+#pragma unroll
+            for (int u = 0; u < NB; ++u) {
+                if (u < pa.m) {
+                    const float2 r2 = reinterpret_cast<const float2*>(qres)[u];
+                    const float ra[2] = {r2.x, r2.y}, bb[2] = {bk[u].x, bk[u].y};
+                    lut[u * 256 + tid] = simd_distance(ra, bb, 2, pa.metric);
+                }
+            }
+        } else {
+            pq_build_lut(pa, qres, lut);
+        }
         __syncthreads();
-        for (int64_t base = 0; base < nrow; base += 256) {
+        // Scores rows base + tid (codes c4 when m16 > 0) and offers them.
+        auto score_batch = [&](int64_t base, const i4v (&c4)[NC]) {
             const int64_t r = base + tid;
             const bool v = r < nrow;
-            const uint32_t* cw = crow + (v ? r : 0) * mw;
             float score = 0.0f;
             if (m16 > 0) {
-                i4v c4[4];
 #pragma unroll
-                for (int c = 0; c < 4; ++c) c4[c] = cur[c];
-                if (base + 256 < nrow) load_codes(r + 256, cur);
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
+                for (int c = 0; c < NC; ++c) {
                     if (c < m16) {
 #pragma unroll
                         for (int w = 0; w < 4; ++w) {
@@ -520,6 +579,7 @@ __global__ __launch_bounds__(256) void ivfpq_scan(PqArgs pa, const float* __rest
                     }
                 }
             } else {
+                const uint32_t* cw = crow + (v ? r : 0) * mw;
                 for (int w = 0; w < mw; ++w) {
                     const uint32_t word = cw[w];
                     score += lut[(4 * w + 0) * 256 + (word & 0xFF)];
@@ -529,6 +589,16 @@ __global__ __launch_bounds__(256) void ivfpq_scan(PqArgs pa, const float* __rest
                 }
             }
             sel.offer(v, score, (uint32_t)(pre + a + r));
+        };
+        for (int64_t base = 0; base < nrow; base += 768) {
+            if (m16 > 0) load_codes(base + 512 + tid, cc);
+            score_batch(base, ca);
+            if (base + 256 >= nrow) break;
+            if (m16 > 0) load_codes(base + 768 + tid, ca);
+            score_batch(base + 256, cb);
+            if (base + 512 >= nrow) break;
+            if (m16 > 0) load_codes(base + 1024 + tid, cb);
+            score_batch(base + 512, cc);
         }
     }
     sel.finish();
@@ -695,15 +765,25 @@ struct mans_ivfpq {
 
 namespace mans {
 
-constexpr int kPqMaxM = 64;      // LUT of m x 256 floats in LDS
 constexpr int kPqMaxKadc = 512;
 
 template <int NCH>
 static void launch_pq_scan(int64_t items, int cap, int kc, const PqArgs& pa, const float* queries,
                            const uint32_t* qidx, const FlatArgs& fa, hipStream_t s) {
     const size_t shmem = sizeof(uint64_t) * 4 * (size_t)cap + sizeof(float) * ((size_t)pa.m * 256 + pa.dim);
-    hipLaunchKernelGGL(ivfpq_scan<NCH>, dim3((unsigned)items), dim3(256), shmem, s, pa, queries, qidx,
-                       kc, cap, fa);
+    // Two-dimensional subvectors, m a multiple of 16 up to 48: codebook
+    // entries in registers (and wave lists of 512 slots compiled for that
+    // size); any other shape takes the general kernel.
+    const bool regs = pa.dsub == 2 && (pa.m & 15) == 0 && pa.m <= 48;
+    if (regs && cap == 512)
+        hipLaunchKernelGGL((ivfpq_scan<NCH, 48, 512>), dim3((unsigned)items), dim3(256), shmem, s,
+                           pa, queries, qidx, kc, cap, fa);
+    else if (regs)
+        hipLaunchKernelGGL((ivfpq_scan<NCH, 48, 0>), dim3((unsigned)items), dim3(256), shmem, s, pa,
+                           queries, qidx, kc, cap, fa);
+    else
+        hipLaunchKernelGGL((ivfpq_scan<NCH, 0, 0>), dim3((unsigned)items), dim3(256), shmem, s, pa,
+                           queries, qidx, kc, cap, fa);
 }
 
 template <int NCH>
@@ -734,18 +814,8 @@ static int ivfpq_search_run(mans_ctx* ctx, const mans_ivfpq* pq, const float* d_
     if (np > 960) return fail(MANS_SEARCH_FAILED, "IVF-PQ: nprobe above 960");
     const int kout = rerank_k > 0 ? (int)rerank_k : (int)k_adc;
 
-    // Probes (BoundedSortedList order).
-    int pkc = np + 64;
-    int pcap = flat_cap_for(pkc);
     hipError_t e = slot->aux1.ensure((size_t)nq * np * sizeof(uint32_t), ctx->fail_alloc);
     if (e != hipSuccess) return hip_fail(e, "IVF-PQ probe workspace");
-    ctx->time_begin(slot, st);
-    hipLaunchKernelGGL(pq_probes, dim3((unsigned)nq), dim3(256),
-                       sizeof(uint64_t) * 4 * (size_t)pcap + sizeof(float) * dim, st, d_q, dim,
-                       (const float*)pq->coarse_t.p, (int)pq->nlist, (int)pq->metric, np, pkc, pcap,
-                       (uint32_t*)slot->aux1.p);
-    e = hipGetLastError();
-    if (e != hipSuccess) return hip_fail(e, "IVF-PQ probes");
     const uint32_t* d_probes = (const uint32_t*)slot->aux1.p;
 
     const int64_t avg_rows = std::max<int64_t>(1, pq->n * np / std::max<int64_t>(1, pq->nlist));
@@ -773,7 +843,11 @@ static int ivfpq_search_run(mans_ctx* ctx, const mans_ivfpq* pq, const float* d_
     e = slot->aux2.ensure(seg_bytes + (size_t)npend * (sizeof(int64_t) + sizeof(float)), ctx->fail_alloc);
     if (e == hipSuccess)
         e = slot->aux3.ensure((size_t)(2 * npend + 1 + items_bound) * sizeof(int32_t), ctx->fail_alloc);
-    if (e == hipSuccess) e = slot->cand.ensure((size_t)items_bound * kc * sizeof(uint64_t), ctx->fail_alloc);
+    // The candidates' workspace first holds the probes' centroid distances.
+    if (e == hipSuccess)
+        e = slot->cand.ensure(std::max((size_t)items_bound * kc * sizeof(uint64_t),
+                                       (size_t)npend * pq->nlist * sizeof(float)),
+                              ctx->fail_alloc);
     if (e == hipSuccess) e = slot->status.ensure((size_t)npend, ctx->fail_alloc);
     if (e == hipSuccess) e = slot->qidx.ensure((size_t)npend * sizeof(int32_t), ctx->fail_alloc);
     if (e == hipSuccess && (slot->counters.bytes < (size_t)npend * sizeof(uint32_t) || slot->counters_dirty)) {
@@ -783,6 +857,33 @@ static int ivfpq_search_run(mans_ctx* ctx, const mans_ivfpq* pq, const float* d_
     }
     if (e == hipSuccess) e = slot->status_h.ensure((size_t)npend);
     if (e != hipSuccess) return hip_fail(e, "IVF-PQ workspace");
+    // Probes (BoundedSortedList order): every query's centroid distances
+    // (in the candidate workspace, free until the scan), then the selection.
+    const int pkc = np + 64;
+    const int pcap = flat_cap_for(pkc);
+    ctx->time_begin(slot, st);
+    {
+        const dim3 grid((unsigned)((pq->nlist + 255) / 256), (unsigned)((nq + kPqDistQ - 1) / kPqDistQ));
+        const size_t shm = sizeof(float) * ((size_t)kPqDistQ * dim + kPqDistQ);
+        float* dists = (float*)slot->cand.p;
+        const float* ct = (const float*)pq->coarse_t.p;
+        const int nl = (int)pq->nlist;
+        switch ((int)pq->metric) {
+        case kMetricL2:
+            hipLaunchKernelGGL(pq_coarse_dist<kMetricL2>, grid, dim3(256), shm, st, d_q, nq, dim, ct, nl, dists);
+            break;
+        case kMetricIP:
+            hipLaunchKernelGGL(pq_coarse_dist<kMetricIP>, grid, dim3(256), shm, st, d_q, nq, dim, ct, nl, dists);
+            break;
+        default:
+            hipLaunchKernelGGL(pq_coarse_dist<kMetricCosine>, grid, dim3(256), shm, st, d_q, nq, dim, ct, nl, dists);
+            break;
+        }
+        hipLaunchKernelGGL(pq_probes, dim3((unsigned)nq), dim3(256), sizeof(uint64_t) * 4 * (size_t)pcap,
+                           st, (const float*)dists, nl, np, pkc, pcap, (uint32_t*)slot->aux1.p);
+    }
+    e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, "IVF-PQ probes");
     int64_t* d_seg = (int64_t*)slot->aux2.p;
     int64_t* d_total = (int64_t*)((char*)slot->aux2.p + seg_bytes);
     float* d_tie = (float*)(d_total + npend);

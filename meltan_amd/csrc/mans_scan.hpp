@@ -179,7 +179,8 @@ __device__ __forceinline__ void block_select_lists(const uint64_t* src, int64_t 
 }
 
 // Wave 0 folds waves 1..3 of the block into its selector (block's kc best).
-__device__ __forceinline__ void block_fold(WaveTopK& sel, uint64_t* lds, int cap) {
+template <class Sel>
+__device__ __forceinline__ void block_fold(Sel& sel, uint64_t* lds, int cap) {
     __syncthreads();
     if ((threadIdx.x >> 6) == 0) {
         const int nw = blockDim.x >> 6;
