@@ -208,7 +208,7 @@ def bench_flat(args, ctx):
             # the dense bf16 peak; the issued rate is twice it.
             avg, launches = kt["flat_gemm"]
             flops = 2.0 * (b * reps / launches) * n * dim
-            roof = roofline_mfma("flat_gemm_bf16x2<384,cosine,8,bounded>", f"flat_{n}x{dim}_b{b}",
+            roof = roofline_mfma("flat_gemm_bf16x2<384,cosine,4,bounded>", f"flat_{n}x{dim}_b{b}",
                                  flops, avg, peak=BF16_MFMA_TFLOPS)
             roof["issued_tflops"] = round(2 * flops / avg / 1e12, 2)
             roof["issued_frac"] = round(2 * flops / avg / 1e12 / BF16_MFMA_TFLOPS, 4)
@@ -626,13 +626,14 @@ def bench_ivfpq(args, ctx):
         def step(s, rerank=rerank):
             pq.search_device(dq.ptr, B, kadc, nprobe, rerank, dd.ptr, di.ptr, stream.handle)
         elapsed = timed(step, 5, 1, hip)
-        kt = kernel_avg(ctx, step, 3, ["ivfpq_scan"], hip)
+        kt = kernel_avg(ctx, step, 3, ["ivfpq_probe", "ivfpq_scan"], hip)
         avg, _ = kt["ivfpq_scan"]
         key = "adc_rerank" if rerank else "adc"
-        out[key] = {"qps": round(B * 5 / elapsed, 1),
-                    "roofline": roofline_hbm("ivfpq_scan", f"ivfpq_{n}x{dim}_b{B}",
-                                             B * cand_per_query * (m + 4), avg),
-                    "cpu_baseline": cpu.get(rerank)}
+        # The event pair brackets the scan launch (with its work-item plan);
+        # the probe selection before it is timed on its own.
+        roof = roofline_hbm("ivfpq_scan", f"ivfpq_{n}x{dim}_b{B}", B * cand_per_query * (m + 4), avg)
+        roof["probe_pass_us"] = round(kt["ivfpq_probe"][0] * 1e6, 2) if kt["ivfpq_probe"][1] else None
+        out[key] = {"qps": round(B * 5 / elapsed, 1), "roofline": roof, "cpu_baseline": cpu.get(rerank)}
         log(f"ivfpq: {key}: {out[key]['qps']} queries/s")
     pq.release()
     corpus.release()

@@ -883,7 +883,9 @@ static int ivfpq_search_run(mans_ctx* ctx, const mans_ivfpq* pq, const float* d_
                            st, (const float*)dists, nl, np, pkc, pcap, (uint32_t*)slot->aux1.p);
     }
     e = hipGetLastError();
+    ctx->time_end(slot, st, "ivfpq_probe");
     if (e != hipSuccess) return hip_fail(e, "IVF-PQ probes");
+    ctx->time_begin(slot, st);
     int64_t* d_seg = (int64_t*)slot->aux2.p;
     int64_t* d_total = (int64_t*)((char*)slot->aux2.p + seg_bytes);
     float* d_tie = (float*)(d_total + npend);

@@ -34,9 +34,9 @@ def _search(ctx, corpus, queries, k, metric):
 
 
 @pytest.mark.parametrize("dim", [64, 96, 128, 192, 256, 384])
-def test_bf3_parity_dims_metrics(gpu_ctx, dim):
+def test_split_parity_dims_metrics(gpu_ctx, dim):
     for n, nq in ((5000, 16), (20011, 130)):
-        print(f"bf3 parity dim={dim} n={n} nq={nq}", flush=True)
+        print(f"split parity dim={dim} n={n} nq={nq}", flush=True)
         corpus = workloads.lcg_vectors(1, n, dim, seed=3 * n + dim)
         queries = workloads.lcg_vectors(1, nq, dim, seed=3 * n + dim + 1)
         norms = oracle.row_norms(corpus)
@@ -45,11 +45,11 @@ def test_bf3_parity_dims_metrics(gpu_ctx, dim):
             for k in (1, 10, 32):
                 gd, gi, launches = _search(gpu_ctx, c, queries, k, metric)
                 assert launches["flat_bound"] == 1 and launches["flat_gemm"] == 1, launches
-                check_flat(corpus, norms, queries, k, metric, gd, gi, f"bf3 dim{dim} n{n} m{metric} k{k}")
+                check_flat(corpus, norms, queries, k, metric, gd, gi, f"split dim{dim} n{n} m{metric} k{k}")
         c.release()
 
 
-def test_bf3_near_duplicates(gpu_ctx):
+def test_split_near_duplicates(gpu_ctx):
     # Rows that differ from each other by a few ulps: the keys' slack covers
     # many rows at once, proofs fail and queries are re-run, and the result
     # must still be exact.
@@ -68,7 +68,7 @@ def test_bf3_near_duplicates(gpu_ctx):
     c.release()
 
 
-def test_bf3_corpus_outside_split_range_keeps_fp32(gpu_ctx):
+def test_split_corpus_outside_split_range_keeps_fp32(gpu_ctx):
     dim, n = 96, 6000
     corpus = workloads.lcg_vectors(0, n, dim, seed=21)
     corpus[17, 5] = 1e-30  # below 2^-50: the split could lose it
@@ -89,7 +89,7 @@ def test_bf3_corpus_outside_split_range_keeps_fp32(gpu_ctx):
     c.release()
 
 
-def test_bf3_query_outside_split_range_is_rerun(gpu_ctx):
+def test_split_query_outside_split_range_is_rerun(gpu_ctx):
     dim, n = 128, 8000
     corpus = workloads.lcg_vectors(1, n, dim, seed=31)
     queries = workloads.lcg_vectors(1, 33, dim, seed=32)
@@ -105,11 +105,11 @@ def test_bf3_query_outside_split_range_is_rerun(gpu_ctx):
     c.release()
 
 
-def test_bf3_mixture_1m_384_batch_1024(gpu_ctx):
+def test_split_mixture_1m_384_batch_1024(gpu_ctx):
     # The batch-1024 workload at full size: every query's ids carry their
     # exact distances in (distance, id) order; a sample of 64 queries equals
     # the oracle's exact top-10.
-    print("bf3 1M x 384 mixture, 1024 queries", flush=True)
+    print("split 1M x 384 mixture, 1024 queries", flush=True)
     db, q = workloads.mixture_1m_384(nq=1024)
     norms = oracle.row_norms(db)
     c = gpu_ctx.upload(db)
