@@ -40,8 +40,9 @@ namespace mans {
 // (kFastLdsBytes with FAST).  FULL: dim == 64 NCH (no partial chunks).
 // PF: one row per group per step with the next step's row loaded while the
 // current one is reduced; otherwise two rows per group per step.  FAST
-// (kc <= 64, cap 128, PF): waves take rows in chunks from a counter, and the
-// threshold merge and lane-per-candidate rescore finish the query.
+// (kc <= 64, cap 128, PF): the threshold merge and lane-per-candidate
+// rescore (flat_fast_merge) finish the query.  rows_per_block sets the
+// grid's block count; the rows go to blocks in strided 32-row tiles.
 template <int NCH, bool FULL, bool PF, bool FAST>
 __global__ __launch_bounds__(256) void flat_scan_f4(
     const float* __restrict__ rows, const float* __restrict__ norms, int64_t n, int dim,
@@ -72,35 +73,28 @@ __global__ __launch_bounds__(256) void flat_scan_f4(
     WaveTopKT<FAST ? 128 : 0> sel;
     sel.init(lds + wave * cap, cap, kc);
 
-    const int64_t start = (int64_t)blockIdx.x * rows_per_block;
-    const int64_t end = start + rows_per_block < n ? start + rows_per_block : n;
-    if constexpr (FAST) {
-        static_assert(PF, "the fast kernel prefetches");
+    // Block b takes the 32-row tiles b, b + nblk, b + 2 nblk, ...: the
+    // blocks in flight read one moving window of the corpus, which keeps
+    // the HBM pages they open close together.
+    const int64_t stride = 32 * (int64_t)gridDim.x;
+    const int64_t first = 32 * (int64_t)blockIdx.x;
+    if constexpr (PF) {
         f4v a[1][NCH], b[1][NCH];
         float va[1], vb[1];
-        scan_load<NCH, FULL, 1>(rows, norms, dim, dim4, start, end, slot, lr, a, va);
-        for (int64_t base = start; base < end; base += 32) {
-            scan_load<NCH, FULL, 1>(rows, norms, dim, dim4, base + 16, end, slot, lr, b, vb);
-            scan_offer<NCH, 1>(a, va, qv, qn, metric, bc, base, end, slot, lr, sel);
-            scan_load<NCH, FULL, 1>(rows, norms, dim, dim4, base + 32, end, slot, lr, a, va);
-            scan_offer<NCH, 1>(b, vb, qv, qn, metric, bc, base + 16, end, slot, lr, sel);
-        }
-    } else if constexpr (PF) {
-        f4v a[1][NCH], b[1][NCH];
-        float va[1], vb[1];
-        scan_load<NCH, FULL, 1>(rows, norms, dim, dim4, start, end, slot, lr, a, va);
-        for (int64_t base = start; base < end; base += 32) {
-            scan_load<NCH, FULL, 1>(rows, norms, dim, dim4, base + 16, end, slot, lr, b, vb);
-            scan_offer<NCH, 1>(a, va, qv, qn, metric, bc, base, end, slot, lr, sel);
-            scan_load<NCH, FULL, 1>(rows, norms, dim, dim4, base + 32, end, slot, lr, a, va);
-            scan_offer<NCH, 1>(b, vb, qv, qn, metric, bc, base + 16, end, slot, lr, sel);
+        scan_load<NCH, FULL, 1>(rows, norms, dim, dim4, first, n, slot, lr, a, va);
+        for (int64_t base = first; base < n; base += stride) {
+            scan_load<NCH, FULL, 1>(rows, norms, dim, dim4, base + 16, n, slot, lr, b, vb);
+            scan_offer<NCH, 1>(a, va, qv, qn, metric, bc, base, n, slot, lr, sel);
+            scan_load<NCH, FULL, 1>(rows, norms, dim, dim4, base + stride, n, slot, lr, a, va);
+            scan_offer<NCH, 1>(b, vb, qv, qn, metric, bc, base + 16, n, slot, lr, sel);
         }
     } else {
-        for (int64_t base = start; base < end; base += 32) {
+        static_assert(!FAST, "the fast kernel prefetches");
+        for (int64_t base = first; base < n; base += stride) {
             f4v a[2][NCH];
             float va[2];
-            scan_load<NCH, FULL, 2>(rows, norms, dim, dim4, base, end, slot, lr, a, va);
-            scan_offer<NCH, 2>(a, va, qv, qn, metric, bc, base, end, slot, lr, sel);
+            scan_load<NCH, FULL, 2>(rows, norms, dim, dim4, base, n, slot, lr, a, va);
+            scan_offer<NCH, 2>(a, va, qv, qn, metric, bc, base, n, slot, lr, sel);
         }
     }
     sel.finish();
@@ -228,10 +222,11 @@ FlatPlan plan_flat(int64_t n, int64_t nq, int kc, int64_t target_blocks) {
         const char* e = std::getenv("MANS_FLAT_BLOCKS");
         return e ? std::max<int64_t>(1, std::atoll(e)) : (int64_t)0;
     }();
-    // About 1024 blocks per launch for large corpora; for smaller ones about
-    // one block per 196 rows (at least 256), so a block's fixed costs
-    // (list, head, merge inputs) stay small next to its rows.
-    const int64_t auto_target = std::min<int64_t>(1024, std::max<int64_t>(256, n / 196));
+    // About 512 blocks per launch for large corpora (two per CU: the merge
+    // reads one list per block); for smaller ones about one block per 196
+    // rows (at least 256), so a block's fixed costs (list, head, merge
+    // inputs) stay small next to its rows.
+    const int64_t auto_target = std::min<int64_t>(512, std::max<int64_t>(256, n / 196));
     const int64_t target = target_blocks > 0 ? target_blocks : (flat_target > 0 ? flat_target : auto_target);
     int64_t want_blocks = (target + nq - 1) / nq;
     int64_t max_blocks = (n + 63) / 64;

@@ -370,97 +370,90 @@ __device__ __forceinline__ void flat_fast_merge_lists(uint64_t* lds, int cap, in
 }
 
 // LDS the threshold merge's rescore needs beyond lds[0, 128): the query
-// (up to 512 floats) and two 32-row pieces of 32 floats per row (rows padded
-// to 36 floats, so the lanes' 16-byte reads spread over the banks).
+// (up to 384 floats) and 32 staged rows of up to 384 floats, each padded by
+// 4 floats so that the lanes' 16-byte reads of one column spread over the
+// banks.
 constexpr int kRescoreRows = 32;
-constexpr int kRescorePiece = 32;
-constexpr int kRescoreStride = 36;
+constexpr int kRescoreMaxDim = 384;
+constexpr int kRescoreStride = kRescoreMaxDim + 4;
 constexpr size_t kFastLdsBytes =
-    128 * sizeof(uint64_t) + (512 + 2 * kRescoreRows * kRescoreStride) * sizeof(float);
+    128 * sizeof(uint64_t) + (kRescoreMaxDim + kRescoreRows * kRescoreStride) * sizeof(float);
 
 // Exact rescore for the threshold merge (kc <= 64, candidates ascending in
-// lds[0, kc)).  Lane c of wave 0 runs candidate c's whole dot product in the
-// dots.c order, and lane 32 the query's own q.q; the rows reach LDS in
-// pieces of 32 floats, loaded by the whole block (eight pieces in flight)
-// and written one piece ahead of the lanes that read them.  32
-// candidates per pass (two passes for kc = 64).  qp: the query in global
-// memory (read with scalar loads).  Wave 0 then sorts the results; outputs
-// and the proof as final_rescore_f4 (flat proof).
+// lds[0, kc), dim <= 64 NCH <= 384).  The whole block loads 32 candidate
+// rows at once into LDS (every load in flight together, one barrier); then
+// lane c of wave 0 runs candidate c's whole dot product in the dots.c order
+// and lane 32 the query's own q.q.  Two passes for kc = 64.  Wave 0 then
+// sorts the results; outputs and the proof as final_rescore_f4 (flat proof).
 template <int NCH, bool FULL>
 __device__ __forceinline__ void final_rescore_fast(const float* __restrict__ qp,
                                                    const float* __restrict__ rows,
                                                    const float* __restrict__ norms, int64_t n,
                                                    int dim, int metric, uint32_t q, uint64_t* lds,
                                                    int kc, const FlatArgs& fa, int status_idx) {
-    constexpr int kMaxPieces = 2 * NCH;  // dim <= 64 NCH
-    constexpr int kWindow = kMaxPieces < 8 ? kMaxPieces : 8;
+    static_assert(16 * NCH * 4 <= kRescoreMaxDim, "rows longer than the staging area");
+    constexpr int kRow4 = 16 * NCH;                    // float4s per row, padded
+    constexpr int kPer = kRescoreRows * kRow4 / 256;   // float4s each thread stages
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int dim4 = FULL ? 16 * NCH : (dim >> 2);
-    const int npieces = FULL ? kMaxPieces : (dim + kRescorePiece - 1) / kRescorePiece;
+    const int dim4 = FULL ? kRow4 : (dim >> 2);
     const uint64_t* top = lds;
     uint64_t* res = lds + 64;
     float* qs = reinterpret_cast<float*>(lds + 128);
-    float* stage = qs + 512;
+    float* stage = qs + kRescoreMaxDim;
     const int ncand = __popcll(__ballot(lane < kc && top[lane] != kEmptySlot));
     for (int i = tid; i < dim4; i += blockDim.x)
         *reinterpret_cast<f4v*>(qs + 4 * i) = *reinterpret_cast<const f4v*>(qp + 4 * i);
-    const int r = tid >> 3, u = tid & 7;  // the row and float4 this thread stages
     float qn = 0.0f;
     for (int pass = 0; pass * kRescoreRows < ncand; ++pass) {
-        const int c = pass * kRescoreRows + r;
-        const bool rv = c < ncand;
-        const uint32_t id = rv ? slot_id(top[c]) : 0u;
-        const float* rp = rows + (int64_t)id * dim;
-        auto load_piece = [&](int pc) {
-            const int off = kRescorePiece * pc + 4 * u;
-            const bool in = rv && (FULL || off < dim);
-            const f4v t = *reinterpret_cast<const f4v*>(rp + (in ? off : 0));
-            return in ? t : f4v{0.f, 0.f, 0.f, 0.f};
-        };
-        f4v v[kWindow];  // pieces in flight: piece pc lives in v[pc % kWindow]
-#pragma unroll
-        for (int pc = 0; pc < kWindow; ++pc) v[pc] = load_piece(pc);
         const int cl = pass * kRescoreRows + lane;  // the candidate lane `lane` rescores
-        float acc = 0.0f;
+        // The candidate's norm, in flight with its row.
+        const float vn_c = wave == 0 && lane < kRescoreRows && cl < ncand && metric != kMetricIP
+                               ? norms[slot_id(top[cl])]
+                               : 0.0f;
+        f4v v[kPer];
 #pragma unroll
-        for (int pc = 0; pc < kMaxPieces; ++pc) {
-            if (!FULL && pc >= npieces) break;
-            float* buf = stage + (pc & 1) * kRescoreRows * kRescoreStride;
-            *reinterpret_cast<f4v*>(buf + r * kRescoreStride + 4 * u) = v[pc % kWindow];
-            if (pc + kWindow < kMaxPieces) v[pc % kWindow] = load_piece(pc + kWindow);
-            __syncthreads();
-            if (wave == 0 && lane <= kRescoreRows) {
-                const float* xr = lane < kRescoreRows ? buf + lane * kRescoreStride
-                                                      : qs + kRescorePiece * pc;
-                const float* yr = qp + kRescorePiece * pc;  // uniform: scalar loads
+        for (int j = 0; j < kPer; ++j) {
+            const int e = tid + 256 * j;
+            const int r = e / kRow4, c4 = e - r * kRow4;
+            const int c = pass * kRescoreRows + r;
+            const bool in = c < ncand && (FULL || c4 < dim4);
+            const uint32_t id = c < ncand ? slot_id(top[c]) : 0u;
+            const f4v t = *reinterpret_cast<const f4v*>(rows + (int64_t)id * dim + (in ? 4 * c4 : 0));
+            v[j] = in ? t : f4v{0.f, 0.f, 0.f, 0.f};
+        }
+        if (pass > 0) __syncthreads();  // the previous pass has read the stage
 #pragma unroll
-                for (int i = 0; i < kRescorePiece / 4; ++i) {
-                    if (!FULL && kRescorePiece * pc + 4 * i >= dim) break;
+        for (int j = 0; j < kPer; ++j) {
+            const int e = tid + 256 * j;
+            const int r = e / kRow4, c4 = e - r * kRow4;
+            *reinterpret_cast<f4v*>(stage + r * kRescoreStride + 4 * c4) = v[j];
+        }
+        __syncthreads();
+        if (wave == 0) {
+            float acc = 0.0f;
+            if (lane <= kRescoreRows) {
+                const float* xr = lane < kRescoreRows ? stage + lane * kRescoreStride : qs;
+                for (int i = 0; i < dim4; ++i) {
                     const f4v x = *reinterpret_cast<const f4v*>(xr + 4 * i);
-                    const f4v y = *reinterpret_cast<const f4v*>(yr + 4 * i);
+                    const f4v y = *reinterpret_cast<const f4v*>(qs + 4 * i);
                     acc = acc + x.x * y.x;
                     acc = acc + x.y * y.y;
                     acc = acc + x.z * y.z;
                     acc = acc + x.w * y.w;
-                    // at most four row reads ahead of the chain (registers)
-                    if (i == 3) __builtin_amdgcn_sched_barrier(0);
                 }
             }
-        }
-        if (wave == 0) {
             if (pass == 0) qn = metric == kMetricIP ? 0.0f : __shfl(acc, kRescoreRows);
             if (lane < kRescoreRows) {
                 uint64_t rs = kEmptySlot;
                 if (cl < ncand) {
                     const uint32_t cid = slot_id(top[cl]);
-                    rs = pack_slot(host_distance(acc, qn, metric == kMetricIP ? 0.0f : norms[cid], metric),
-                                   cid);
+                    rs = pack_slot(host_distance(acc, qn, vn_c, metric), cid);
                 }
                 res[cl] = rs;
             }
         }
-        __syncthreads();  // the stage buffers are reused by the next pass
     }
+    __syncthreads();
     if (wave == 0) {
         uint64_t w[1];
         w[0] = lane < ncand ? res[lane] : kEmptySlot;
