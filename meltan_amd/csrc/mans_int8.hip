@@ -20,6 +20,7 @@
 //     proof-checked search returns the exact flat scan's result, which is
 //     what a proven reference round returns.
 #include <algorithm>
+#include <map>
 #include <cstdlib>
 #include <cstring>
 #include <vector>
@@ -415,17 +416,23 @@ static void launch_int8_scan(const FlatPlan& p, const Int8Planes& pl, const floa
                        p.rows_per_block, proof, fa, sb);
 }
 
-// Threshold-collect scan (one query per grid row, every query of the
-// launch).  Every row whose slot is at or below the query's bound (the
-// kc-th smallest slot of a sample of rows, so the kc smallest slots of all
-// rows are among them) is gathered by its block, which rescores it exactly
-// (the dots.c order) and appends its slot and its exact (distance, id)
-// slot to the query's buffers.  The last block of the query selects the kc
-// smallest slots (radix select), sorts their exact slots and writes the
-// first k and the proof status.  A block with more than kCollectLdsSlots
-// such rows, or more than I8Collect::ccap of them in all, gives the status
-// kStatusReselect and nothing else is written (the caller selects again
-// with the lists).
+// Threshold-collect scan (one query per grid row; qidx, nullable, maps grid
+// rows to queries).  Every row whose slot is at or below the row's bound
+// (from a sample of rows: at least bound_kc rows lie at or below it) is
+// gathered by its block, which rescores it exactly (the dots.c order) and
+// appends its slot and its exact (distance, id) slot to the row's buffers.
+// The last block of the grid row then runs the budget rounds of
+// BoundedExactScan.search (BoundedExactScan.swift:96-121) on what was
+// gathered: with `total` rows gathered at or below the bound, the budget
+// smallest slots of the whole corpus are among them whenever budget <=
+// total, so each round selects them (radix select), takes the k smallest
+// exact slots of the selection and checks the proof; a failed proof grows
+// the budget 4x and selects again.  Status: bits 0-1 the outcome (0 done, 1
+// the proof still fails and the next budget exceeds `total`: the host scans
+// again at budget kc 4^rounds; kStatusReselect: no round could run), bits
+// 2-7 the rounds run.  A block with more than kCollectLdsSlots such rows, or
+// more than I8Collect::ccap of them in all, gives kStatusReselect and
+// nothing else is written (the caller selects again with the lists).
 struct I8Collect {
     const uint64_t* qbound;  // [nq]
     uint64_t* cbuf;          // [nq][ccap] slots (int8 keys)
@@ -434,26 +441,29 @@ struct I8Collect {
 };
 constexpr int kCollectLdsSlots = 4096;  // rows gathered per block; candidates selected in LDS
 constexpr size_t kCollectShmem = sizeof(uint64_t) * (256 + kCollectLdsSlots);
+constexpr int64_t kCollectMaxCap = 65536;  // gathered rows per query
+constexpr int64_t kCollectMaxQueries = 64;  // queries per collect launch
 
-// grid (nblk, nq); block 256; dynamic LDS kCollectShmem; kc <= 256.
+// grid (nblk, nq_launch); block 256; dynamic LDS kCollectShmem.
 template <int NCH>
 __global__ __launch_bounds__(256) void int8_collect(
     Int8Planes pl, const float* __restrict__ rows, const float* __restrict__ norms, int64_t n,
-    int dim, const float* __restrict__ queries, const int8_t* __restrict__ qcodes,
-    const Int8QueryCoef* __restrict__ coefs, int metric, int kc, int64_t rows_per_block,
-    int proof, FlatArgs fa, I8Collect cl) {
+    int dim, const float* __restrict__ queries, const uint32_t* __restrict__ qidx,
+    const int8_t* __restrict__ qcodes, const Int8QueryCoef* __restrict__ coefs, int metric,
+    int kc, int64_t rows_per_block, int proof, FlatArgs fa, I8Collect cl) {
     constexpr int NC8 = (NCH + 1) / 2;
     extern __shared__ uint64_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t q = blockIdx.y;
+    const uint32_t y = blockIdx.y;
+    const uint32_t q = qidx ? qidx[y] : y;
     const Int8QueryCoef coef = coefs[q];
     i4v qc[NC8];
     int8_query_chunks<NC8>(qcodes, q, pl.stride, qc);
-    const uint64_t bound = cl.qbound[q];
-    uint32_t* arrive = fa.counters + (int64_t)q * (fa.ngroups + 1);
+    const uint64_t bound = cl.qbound[y];
+    uint32_t* arrive = fa.counters + (int64_t)y * (fa.ngroups + 1);
     uint32_t* appended = arrive + 1;
-    uint64_t* cbuf = cl.cbuf + (int64_t)q * cl.ccap;
-    uint64_t* ebuf = cl.ebuf + (int64_t)q * cl.ccap;
+    uint64_t* cbuf = cl.cbuf + (int64_t)y * cl.ccap;
+    uint64_t* ebuf = cl.ebuf + (int64_t)y * cl.ccap;
     const int64_t start = (int64_t)blockIdx.x * rows_per_block;
     const int64_t end = start + rows_per_block < n ? start + rows_per_block : n;
     uint64_t* top = lds;         // 256 slots (the last block's selection)
@@ -526,7 +536,7 @@ __global__ __launch_bounds__(256) void int8_collect(
     __syncthreads();
     const int64_t total = s_total;
     if (total > cl.ccap) {
-        if (tid == 0) fa.status[q] = kStatusReselect;
+        if (tid == 0) fa.status[y] = kStatusReselect;
         return;
     }
     __shared__ uint32_t hist[256];
@@ -534,68 +544,94 @@ __global__ __launch_bounds__(256) void int8_collect(
     const bool in_lds = total <= kCollectLdsSlots;
     if (in_lds)
         for (int64_t i = tid; i < total; i += blockDim.x) cand[i] = load_shared_slot(cbuf + i);
-    if (tid == 0) ntop = 0;
     __syncthreads();
     auto get = [&](int64_t i) { return in_lds ? cand[i] : load_shared_slot(cbuf + i); };
-    uint64_t kth;
-    const uint64_t cut = block_radix_cut(get, total, kc, hist, &kth);
-    // The selected rows' exact slots, and the largest selected slot (the
-    // kc-th, or the last of fewer).
-    uint64_t mx = 0;
-    for (int64_t i = tid; i < total; i += blockDim.x) {
-        const uint64_t s = get(i);
-        if (s <= cut) {
-            const int p = atomicAdd(&ntop, 1);
-            if (p < 256) top[p] = load_shared_slot(ebuf + i);  // at most kc <= 256 (distinct slots)
-            mx = s > mx ? s : mx;
+    int64_t budget = kc;
+    for (int round = 1;; ++round) {
+        if (budget > total && total < n) {
+            // The gathered rows no longer hold the budget smallest slots.
+            if (tid == 0) fa.status[y] = round == 1 ? kStatusReselect : (uint8_t)(1 | ((round - 1) << 2));
+            return;
         }
-    }
-    const uint64_t cut_key = block_reduce_u64<true>(mx);  // (its barriers order top[] too)
-    const int ncand = ntop < 256 ? ntop : 256;
-    int sort_n = 64;
-    while (sort_n < ncand) sort_n <<= 1;
-    for (int i = ncand + tid; i < sort_n; i += blockDim.x) top[i] = kEmptySlot;
-    __syncthreads();
-    if (tid < 64) wave_bitonic_sort(top, sort_n);
-    __syncthreads();
-    const int kout = fa.k < ncand ? fa.k : ncand;
-    for (int i = tid; i < fa.k_stride; i += blockDim.x) {
-        float dv = kFltMax;
-        uint32_t id = kEmptyId;
-        if (i < kout) {
-            id = slot_id(top[i]);
-            dv = slot_key(top[i]);
+        // The selection: the budget smallest slots (every gathered row when
+        // they are all there is), and the largest of them.
+        const int64_t nsel = budget < total ? budget : total;
+        uint64_t kth;
+        const uint64_t cut = block_radix_cut(get, total, (int)nsel, hist, &kth);
+        if (cut == kEmptySlot) {
+            uint64_t mx = 0;
+            for (int64_t i = tid; i < total; i += blockDim.x) {
+                const uint64_t s = get(i);
+                mx = s > mx ? s : mx;
+            }
+            kth = block_reduce_u64<true>(mx);
         }
-        fa.out_dist[(int64_t)q * fa.k_stride + i] = dv;
-        fa.out_ids[(int64_t)q * fa.k_stride + i] = id;
-    }
-    if (tid == 0) {
-        const float cutoff = ncand > 0 ? slot_key(cut_key) : 0.0f;
-        const bool all_rows = (int64_t)ncand >= n;
+        // The k smallest exact slots of the selection, sorted.
+        const int kout = (int64_t)fa.k < nsel ? fa.k : (int)nsel;
+        auto gete = [&](int64_t i) {
+            return get(i) <= cut ? load_shared_slot(ebuf + i) : kEmptySlot;
+        };
+        uint64_t ekth;
+        const uint64_t ecut = block_radix_cut(gete, total, kout, hist, &ekth);
+        if (tid == 0) ntop = 0;
+        __syncthreads();
+        for (int64_t i = tid; i < total; i += blockDim.x) {
+            if (get(i) > cut) continue;
+            const uint64_t e = load_shared_slot(ebuf + i);
+            if (e <= ecut) {
+                const int p = atomicAdd(&ntop, 1);
+                if (p < 256) top[p] = e;  // kout <= k <= 256 distinct slots
+            }
+        }
+        __syncthreads();
+        const int nout = ntop < kout ? ntop : kout;
+        int sort_n = 64;
+        while (sort_n < nout) sort_n <<= 1;
+        for (int i = nout + tid; i < sort_n; i += blockDim.x) top[i] = kEmptySlot;
+        __syncthreads();
+        if (tid < 64) wave_bitonic_sort(top, sort_n);
+        __syncthreads();
+        const float cutoff = slot_key(kth);
+        const float tau = nout > 0 ? slot_key(top[nout - 1]) : 0.0f;
+        const bool all_rows = nsel >= n;
         bool ok;
         if (proof == kProofNone) {
             ok = true;
         } else if (proof == kProofMargin) {
-            // BoundedExactScan.swift:108-113
-            const float tau = kout > 0 ? slot_key(top[kout - 1]) : 0.0f;
+            // BoundedExactScan.swift:101-113
             double margin = fabs((double)tau) * 1e-6;
             margin = margin < 1e-7 ? 1e-7 : margin;
-            ok = all_rows || ncand < fa.k || (double)cutoff >= (double)tau + margin;
+            ok = all_rows || nsel < fa.k || (double)cutoff >= (double)tau + margin;
         } else {
-            ok = all_rows || (kout > 0 && cutoff >= slot_key(top[kout - 1]));
+            ok = all_rows || (nout > 0 && cutoff >= tau);
         }
-        fa.status[q] = ok ? 0 : 1;
+        if (ok) {
+            for (int i = tid; i < fa.k_stride; i += blockDim.x) {
+                float dv = kFltMax;
+                uint32_t id = kEmptyId;
+                if (i < nout) {
+                    id = slot_id(top[i]);
+                    dv = slot_key(top[i]);
+                }
+                fa.out_dist[(int64_t)q * fa.k_stride + i] = dv;
+                fa.out_ids[(int64_t)q * fa.k_stride + i] = id;
+            }
+            if (tid == 0) fa.status[y] = (uint8_t)(round << 2);
+            return;
+        }
+        budget = budget * 4 < n ? budget * 4 : n;
+        __syncthreads();  // top[] and ntop are rewritten by the next round
     }
 }
 
 template <int NCH>
 static hipError_t launch_int8_collect(const FlatPlan& p, const Int8Planes& pl, const float* rows,
                                       const float* norms, int64_t n, int dim, const float* queries,
-                                      int64_t nq, const int8_t* qcodes, const Int8QueryCoef* coefs,
-                                      int metric, int kc, int proof, const FlatArgs& fa,
-                                      const I8Collect& cl, hipStream_t s) {
+                                      const uint32_t* qidx, int64_t nq, const int8_t* qcodes,
+                                      const Int8QueryCoef* coefs, int metric, int kc, int proof,
+                                      const FlatArgs& fa, const I8Collect& cl, hipStream_t s) {
     hipLaunchKernelGGL(int8_collect<NCH>, dim3(p.nblk, (unsigned)nq), dim3(256), kCollectShmem, s,
-                       pl, rows, norms, n, dim, queries, qcodes, coefs, metric, kc,
+                       pl, rows, norms, n, dim, queries, qidx, qcodes, coefs, metric, kc,
                        p.rows_per_block, proof, fa, cl);
     return hipGetLastError();
 }
@@ -1300,30 +1336,42 @@ static int int8_search_run(mans_ctx* ctx, mans_corpus* c, const float* d_q, int6
         return MANS_OK;
     };
 
-    // Streaming rounds over every query at kc <= 256 take the threshold-
-    // collect scan when the sampled bound applies: blocks of at least 256
-    // rows, at least kc blocks per query.
+    // Rounds at budgets up to kInt8MaxBudget take the threshold-collect scan
+    // when the sampled bound applies: blocks of at least 256 rows.  The
+    // bound is the min(kc, nblk / 2)-th smallest block minimum of the
+    // sample.
     static const int64_t collect_target = [] {
         const char* e = std::getenv("MANS_INT8_BLOCKS");
         return e ? std::max<int64_t>(1, std::atoll(e)) : (int64_t)512;
     }();
     auto collect_plan = [&](int64_t kc, FlatPlan* p) {
-        if (kc > 256 || !int8_collect_enabled() || !int8_sampled_bounds()) return false;
-        *p = plan_flat(n, 1, (int)kc, collect_target);
-        return p->rows_per_block >= 256 && p->nblk >= kc;
+        if (kc > kInt8MaxBudget || !int8_collect_enabled() || !int8_sampled_bounds()) return false;
+        *p = plan_flat(n, 1, (int)std::min<int64_t>(kc, 256), collect_target);
+        return p->rows_per_block >= 256 && p->nblk >= 2;
     };
-    // One threshold-collect round over every query at candidate count kc;
-    // queries whose bound let more rows through than the candidate buffer
-    // holds repeat the round with the lists.
-    auto collect_round = [&](const FlatPlan& p, int64_t kc, std::vector<uint32_t>& grow) -> int {
+    // One threshold-collect launch over `idx` (empty: every query) starting
+    // at budget kc; appends (query, next budget) for the queries whose proof
+    // still fails.  Queries whose bound let more rows through than the
+    // buffers hold repeat the round with the lists.
+    auto collect_round = [&](const FlatPlan& p, const std::vector<uint32_t>& idx, int64_t kc,
+                             std::vector<std::pair<uint32_t, int64_t>>& next) -> int {
+        const int64_t cnt = idx.empty() ? nq : (int64_t)idx.size();
         FlatBuffers fb;
-        hipError_t e = prepare_flat_buffers(ctx, slot, p, nq, st, &fb);
-        // Candidate buffers: slots, then exact slots, ccap = nblk kc each.
-        const int64_t ccap = (int64_t)p.nblk * p.kc;
+        hipError_t e = prepare_flat_buffers(ctx, slot, p, cnt, st, &fb);
+        // Candidate buffers: slots, then exact slots, ccap each.
+        const int64_t ccap = std::min<int64_t>((int64_t)p.nblk * std::max<int64_t>(kc, 256), kCollectMaxCap);
         if (e == hipSuccess)
-            e = slot->cand.ensure((size_t)nq * 2 * ccap * sizeof(uint64_t), ctx->fail_alloc);
+            e = slot->cand.ensure((size_t)cnt * 2 * ccap * sizeof(uint64_t), ctx->fail_alloc);
         fb.cand = (uint64_t*)slot->cand.p;
-        if (e == hipSuccess) e = slot->status_h.ensure((size_t)nq);
+        if (e == hipSuccess) e = slot->status_h.ensure((size_t)cnt);
+        const uint32_t* d_qidx = nullptr;
+        if (e == hipSuccess && !idx.empty()) {
+            e = slot->qidx.ensure(idx.size() * sizeof(uint32_t), ctx->fail_alloc);
+            if (e == hipSuccess)
+                e = hipMemcpyAsync(slot->qidx.p, idx.data(), idx.size() * sizeof(uint32_t),
+                                   hipMemcpyHostToDevice, st);
+            d_qidx = (const uint32_t*)slot->qidx.p;
+        }
         if (e != hipSuccess) return hip_fail(e, "int8 scan workspace");
         FlatArgs fa = {};
         fa.cand = fb.cand;
@@ -1338,35 +1386,36 @@ static int int8_search_run(mans_ctx* ctx, mans_corpus* c, const float* d_q, int6
         fa.ngroups = p.ngroups;
         auto launch = [&](const FlatPlan& lp, const I8ScanBounds& sb) {
             switch (nch) {
-            case 1: launch_int8_scan<1>(lp, pl, rows, norms, n, dim, d_q, nullptr, nq, qcodes, coefs, (int)metric, proof, fa, sb, st); break;
-            case 2: launch_int8_scan<2>(lp, pl, rows, norms, n, dim, d_q, nullptr, nq, qcodes, coefs, (int)metric, proof, fa, sb, st); break;
-            case 3: launch_int8_scan<3>(lp, pl, rows, norms, n, dim, d_q, nullptr, nq, qcodes, coefs, (int)metric, proof, fa, sb, st); break;
-            case 4: launch_int8_scan<4>(lp, pl, rows, norms, n, dim, d_q, nullptr, nq, qcodes, coefs, (int)metric, proof, fa, sb, st); break;
-            case 6: launch_int8_scan<6>(lp, pl, rows, norms, n, dim, d_q, nullptr, nq, qcodes, coefs, (int)metric, proof, fa, sb, st); break;
-            default: launch_int8_scan<8>(lp, pl, rows, norms, n, dim, d_q, nullptr, nq, qcodes, coefs, (int)metric, proof, fa, sb, st); break;
+            case 1: launch_int8_scan<1>(lp, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, proof, fa, sb, st); break;
+            case 2: launch_int8_scan<2>(lp, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, proof, fa, sb, st); break;
+            case 3: launch_int8_scan<3>(lp, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, proof, fa, sb, st); break;
+            case 4: launch_int8_scan<4>(lp, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, proof, fa, sb, st); break;
+            case 6: launch_int8_scan<6>(lp, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, proof, fa, sb, st); break;
+            default: launch_int8_scan<8>(lp, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, proof, fa, sb, st); break;
             }
             return hipGetLastError();
         };
         ctx->time_begin(slot, st);
         const bool prep = !prep_done && dim <= kI8MaxDim;
         if (!prep_done && !prep) e = launch_prep();
-        if (e == hipSuccess) e = sampled_bounds(p, kc, nq, launch, prep);
+        const int64_t bound_kc = std::min<int64_t>(kc, std::max<int64_t>(1, p.nblk / 2));
+        if (e == hipSuccess) e = sampled_bounds(p, bound_kc, cnt, launch, prep);
         prep_done = true;
         ctx->time_end(slot, st, "int8_bound");
         I8Collect cl;
-        cl.qbound = (const uint64_t*)slot->bounds.p + (size_t)nq * p.nblk;
+        cl.qbound = (const uint64_t*)slot->bounds.p + (size_t)cnt * p.nblk;
         cl.cbuf = fb.cand;
-        cl.ebuf = fb.cand + (size_t)nq * ccap;
+        cl.ebuf = fb.cand + (size_t)cnt * ccap;
         cl.ccap = ccap;
         ctx->time_begin(slot, st);
         if (e == hipSuccess) {
             switch (nch) {
-            case 1: e = launch_int8_collect<1>(p, pl, rows, norms, n, dim, d_q, nq, qcodes, coefs, (int)metric, (int)kc, proof, fa, cl, st); break;
-            case 2: e = launch_int8_collect<2>(p, pl, rows, norms, n, dim, d_q, nq, qcodes, coefs, (int)metric, (int)kc, proof, fa, cl, st); break;
-            case 3: e = launch_int8_collect<3>(p, pl, rows, norms, n, dim, d_q, nq, qcodes, coefs, (int)metric, (int)kc, proof, fa, cl, st); break;
-            case 4: e = launch_int8_collect<4>(p, pl, rows, norms, n, dim, d_q, nq, qcodes, coefs, (int)metric, (int)kc, proof, fa, cl, st); break;
-            case 6: e = launch_int8_collect<6>(p, pl, rows, norms, n, dim, d_q, nq, qcodes, coefs, (int)metric, (int)kc, proof, fa, cl, st); break;
-            default: e = launch_int8_collect<8>(p, pl, rows, norms, n, dim, d_q, nq, qcodes, coefs, (int)metric, (int)kc, proof, fa, cl, st); break;
+            case 1: e = launch_int8_collect<1>(p, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, (int)kc, proof, fa, cl, st); break;
+            case 2: e = launch_int8_collect<2>(p, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, (int)kc, proof, fa, cl, st); break;
+            case 3: e = launch_int8_collect<3>(p, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, (int)kc, proof, fa, cl, st); break;
+            case 4: e = launch_int8_collect<4>(p, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, (int)kc, proof, fa, cl, st); break;
+            case 6: e = launch_int8_collect<6>(p, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, (int)kc, proof, fa, cl, st); break;
+            default: e = launch_int8_collect<8>(p, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, (int)kc, proof, fa, cl, st); break;
             }
         }
         ctx->time_end(slot, st, "int8_scan");
@@ -1377,19 +1426,26 @@ static int int8_search_run(mans_ctx* ctx, mans_corpus* c, const float* d_q, int6
         }
         std::vector<uint32_t> redo;
         const uint8_t* sh = (const uint8_t*)slot->status_h.p;
-        for (int64_t i = 0; i < nq; ++i) {
-            if (sh[i] == kStatusReselect) {
-                redo.push_back((uint32_t)i);
+        for (int64_t i = 0; i < cnt; ++i) {
+            const uint32_t qi = idx.empty() ? (uint32_t)i : idx[i];
+            const int outcome = sh[i] & 3, ran = sh[i] >> 2;
+            if (outcome == kStatusReselect) {
+                redo.push_back(qi);
                 continue;
             }
-            rounds[i] += 1;
-            if (sh[i]) grow.push_back((uint32_t)i);
+            rounds[qi] += ran;
+            if (outcome == 1) {
+                int64_t b = kc;
+                for (int r = 0; r < ran; ++r) b = std::min<int64_t>(b * 4, n);
+                next.emplace_back(qi, b);
+            }
         }
         ctx->reselects += (int64_t)redo.size();
         if (!redo.empty()) {
+            std::vector<uint32_t> grow;
             int rc = stream_round(redo, kc, true, grow);
             if (rc != MANS_OK) return rc;
-            std::sort(grow.begin(), grow.end());
+            for (uint32_t qi : grow) next.emplace_back(qi, std::min<int64_t>(kc * 4, n));
         }
         return MANS_OK;
     };
@@ -1463,43 +1519,61 @@ static int int8_search_run(mans_ctx* ctx, mans_corpus* c, const float* d_q, int6
         return MANS_OK;
     };
 
-    std::vector<uint32_t> pending;  // empty = all queries
+    // Budgets still to run, each with its queries (an empty list at the
+    // first budget: every query).  Budgets grow 4x per failed proof
+    // (BoundedExactScan.swift:115-118); past kInt8MaxBudget the exact scan
+    // finishes the remaining queries.
+    std::map<int64_t, std::vector<uint32_t>> todo;
+    todo[kc] = {};
     bool first = true;
-    for (;;) {
-        if (kc > kInt8MaxBudget) {
+    while (!todo.empty()) {
+        const int64_t bkc = todo.begin()->first;
+        std::vector<uint32_t> idx = std::move(todo.begin()->second);
+        todo.erase(todo.begin());
+        if (bkc > kInt8MaxBudget) {
             if (mode == 1)
                 return fail(MANS_PIPELINE_UNAVAILABLE, "int8 scan: fixed budget above 1024");
-            std::vector<uint32_t> all;
-            const std::vector<uint32_t>* idx = &pending;
-            if (pending.empty()) {
-                all.resize((size_t)nq);
-                for (int64_t i = 0; i < nq; ++i) all[i] = (uint32_t)i;
-                idx = &all;
+            if (idx.empty()) {
+                idx.resize((size_t)nq);
+                for (int64_t i = 0; i < nq; ++i) idx[i] = (uint32_t)i;
             }
-            for (uint32_t qi : *idx) rounds[qi] += 1;
-            return finish(int8_exact_fallback(ctx, c, d_q, *idx, k, metric, d_dist, d_ids, st, slot));
+            for (auto& rest : todo) idx.insert(idx.end(), rest.second.begin(), rest.second.end());
+            std::sort(idx.begin(), idx.end());
+            for (uint32_t qi : idx) rounds[qi] += 1;
+            return finish(int8_exact_fallback(ctx, c, d_q, idx, k, metric, d_dist, d_ids, st, slot));
         }
-        std::vector<uint32_t> next;
+        std::vector<std::pair<uint32_t, int64_t>> next;
         I8GemmPlan gp;
-        int rc;
         FlatPlan cp;
-        const bool gemm = first && plan_i8gemm(n, stride, nq, kc, &gp);
-        const bool collect = !gemm && pending.empty() && collect_plan(kc, &cp);
+        int rc;
+        const bool gemm = first && idx.empty() && plan_i8gemm(n, stride, nq, bkc, &gp);
+        // Many queries at once keep HBM busy on the list scan; the collect
+        // launch serves single queries and small groups.
+        const bool collect =
+            !gemm && (idx.empty() ? nq : (int64_t)idx.size()) <= kCollectMaxQueries &&
+            collect_plan(bkc, &cp);
         if (!prep_done && !collect) {
             e = launch_prep();
             if (e != hipSuccess) return hip_fail(e, "int8 query prep");
         }
-        if (gemm) rc = gemm_round(gp, kc, next);
-        else if (collect) rc = collect_round(cp, kc, next);
-        else rc = stream_round(pending, kc, !first, next);
+        if (collect) {
+            rc = collect_round(cp, idx, bkc, next);
+        } else {
+            std::vector<uint32_t> grow;
+            rc = gemm ? gemm_round(gp, bkc, grow) : stream_round(idx, bkc, !first, grow);
+            for (uint32_t qi : grow) next.emplace_back(qi, std::min<int64_t>(bkc * 4, n));
+        }
         if (rc != MANS_OK) return rc;
         first = false;
-        if (next.empty()) return finish(MANS_OK);
-        if (kc >= n) return fail(MANS_SEARCH_FAILED, "int8 scan: proof failed with every row selected");
-        pending.swap(next);
-        kc = std::min<int64_t>(kc * 4, n);
-        ctx->proof_retries += (int64_t)pending.size();
+        for (const auto& qn : next) {
+            if (qn.second <= bkc)  // the budget cannot grow: every row was selected
+                return fail(MANS_SEARCH_FAILED, "int8 scan: proof failed with every row selected");
+            todo[qn.second].push_back(qn.first);
+            ctx->proof_retries += 1;
+        }
+        for (auto& t : todo) std::sort(t.second.begin(), t.second.end());
     }
+    return finish(MANS_OK);
 }
 
 }  // namespace mans

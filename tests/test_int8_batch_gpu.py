@@ -129,3 +129,27 @@ def test_int8_batched_mixture_1m_384(gpu_ctx):
     ref = _oracle_rows(db, norms, planes, q[sample], 10, COS, mode=1, budget=100)
     _assert_same(gd[sample], gi[sample], ref, 10, "1M mode1 batch")
     c.release()
+
+
+def test_int8_batched_mode0_pending_queries_collect(gpu_ctx):
+    # Mode 0 on the 1M x 384 mixture with 24 queries: the first round (budget
+    # 256) runs on i8 MFMA; the queries whose proof fails there (budget 1024
+    # on this mixture) go to one threshold-collect launch over just those
+    # queries, whose last blocks run the later budget rounds on the rows
+    # they gathered.  Results equal the exact flat search and the round
+    # counts equal the oracle's restatement of BoundedExactScan.
+    print("int8 batched mode 0, 1M x 384 mixture, 24 queries", flush=True)
+    db, q = workloads.mixture_1m_384(nq=24)
+    c = gpu_ctx.upload(db)
+    gd, gi, rounds, launches = _batched(gpu_ctx, c, q, 10, COS, 0, 0)
+    assert launches["int8_gemm"] == 1 and launches["int8_scan"] >= 1, launches
+    fd, fi = c.flat_search(q, 10, COS)
+    assert np.array_equal(gd, fd) and np.array_equal(gi, fi)
+    assert np.any(rounds > 1)
+    norms = oracle.row_norms(db)
+    planes = oracle.int8_build(db)
+    for i in (0, 7, 23):
+        final = oracle.int8_search(db, norms, planes, q[i], 10, COS)[2]
+        assert rounds[i] == _rounds_for(final, 10, len(db)), f"query {i}"
+    c.release()
+

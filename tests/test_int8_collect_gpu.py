@@ -1,15 +1,18 @@
 """Parity of the threshold-collect int8 scan.
 
-Single queries and small batches over corpora of at least 256 rows per
-block (about 131,000 rows and up) and candidate counts up to 256 run in two
-launches: a sampled launch over a sixteenth of each block's rows gives each
-query a bound (the kc-th smallest block minimum, an upper bound on its kc-th
-smallest slot), then every row at or below the bound is collected and the
-query's last block selects the kc smallest (radix select), rescores them in
-the dots.c order and writes the results.  The answers must equal the
-oracle's restatement of BoundedExactScan bit for bit, as the list-based scan
-does.  A bound that lets more rows through than the candidate buffer holds
-(many equal keys) sends the query back to the list-based scan.
+Single queries and small groups (up to 64 queries) over corpora of at least
+256 rows per block (about 131,000 rows and up), at budgets up to 1024, run
+in two launches: a sampled launch over a sixteenth of each block's rows
+gives each query a bound (the min(kc, nblk / 2)-th smallest block minimum:
+at least that many rows lie at or below it), then every row at or below the
+bound is collected and rescored, and the query's last block runs the budget
+rounds of BoundedExactScan on what was collected: while the budget is at
+most the number of rows collected, the budget smallest slots are among them,
+so each round selects them (radix select), takes the k best exact slots and
+checks the proof.  The answers and the round counts must equal the oracle's
+restatement of BoundedExactScan bit for bit, as the list-based scan does.  A
+bound that lets more rows through than the candidate buffer holds (many
+equal keys) sends the query back to the list-based scan.
 """
 import numpy as np
 import pytest

@@ -174,6 +174,14 @@ def test_int8_mixture_1m_384_sample(gpu_ctx):
     assert np.array_equal(gi, fi)
     norms = oracle.row_norms(db)
     planes = oracle.int8_build(db)
+    # Single queries: one collect launch whose last block runs every budget
+    # round the proof needs; the round counts equal the oracle's.
+    from test_int8_batch_gpu import _rounds_for
+    for i in range(3):
+        _, gi1, r1 = c.int8_search(q[i:i + 1], 10, COS, mode=0)
+        final = oracle.int8_search(db, norms, planes, q[i], 10, COS)[2]
+        assert r1[0] == _rounds_for(final, 10, len(db)), f"query {i}"
+        assert np.array_equal(gi1[0], fi[i])
     gd1, gi1, _ = c.int8_search(q[:3], 10, COS, mode=1, budget=100)
     ref = _oracle_rows(db, norms, planes, q[:3], 10, COS, mode=1, budget=100)
     _assert_same(gd1, gi1, ref, 10, "1M mode1")
