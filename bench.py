@@ -520,17 +520,28 @@ def bench_ivf(args, ctx):
             if not (np.array_equal(gp[i], op) and np.array_equal(gd[i, :len(od)], od)):
                 raise SystemExit("IVF parity gate failed")
         cand_rows = int(sum(sizes[gp[i]].sum() for i in range(B)))
+        probed = np.unique(gp[:B].ravel())
+        list_rows = int(sizes[probed].sum())
 
         def step(s, nprobe=nprobe):
             ivf.search_device(dq.ptr, B, k, nprobe, dd.ptr, di.ptr, stream.handle)
         elapsed = timed(step, 5, 1, hip)
-        kt = kernel_avg(ctx, step, 3, ["ivf_scan"], hip)
-        avg, _ = kt["ivf_scan"]
+        kt = kernel_avg(ctx, step, 3, ["ivf_probe", "ivf_lm", "ivf_scan"], hip)
+        # The list-major scan reads every probed list once per batch: its
+        # algorithmic bytes are the distinct probed lists' rows, norms and
+        # ids; it forms cand_rows (query, row) dots of 2 dim flop each.
+        avg, _ = kt["ivf_lm"]
+        roof = roofline_hbm("ivf_lm_scan<2> + ivf_lm_merge<2>", f"ivf_{n}x{dim}_np{nprobe}_b{B}",
+                            list_rows * (dim * 4 + 4 + 4), avg)
+        roof["pair_tflops"] = round(2.0 * dim * cand_rows / avg / 1e12, 2)
+        roof["probe_pass_us"] = round(kt["ivf_probe"][0] * 1e6, 2) if kt["ivf_probe"][1] else None
+        roof["proof_rounds_us"] = (round((kt["ivf_scan"][0] - avg) * 1e6, 2)
+                                   if kt["ivf_scan"][1] else None)
         out[f"nprobe{nprobe}"] = {
             "qps": round(B * 5 / elapsed, 1),
             "candidates_per_query": round(cand_rows / B, 1),
-            "roofline": roofline_hbm("ivf_scan<2>", f"ivf_{n}x{dim}_np{nprobe}_b{B}",
-                                     cand_rows * (dim * 4 + 4 + 4), avg)}
+            "distinct_lists": int(probed.size),
+            "roofline": roof}
         if not args.no_cpu:
             # IVFFlatSearch.search per query (scanProbedLists,
             # IVFFlatSearch.swift:214-291) over the same lists, queries

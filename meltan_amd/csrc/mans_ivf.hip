@@ -14,6 +14,7 @@
 // with the list ids as the reported ids, and the proof, re-run with a
 // larger candidate count where it fails.
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -31,6 +32,7 @@ struct mans_ivf {
     mans::DevBuf list_ids;        // uint32 [n]
     mans::DevBuf packed;          // f32 [n][dim], rows in list order
     mans::DevBuf packed_norms;    // f32 [n]
+    mans::DevBuf cent_t;          // f32 [dim][nlist], the centroids transposed
     std::vector<int64_t> h_offsets;
     ~mans_ivf() {
         if (cent) mans_corpus_release(cent);
@@ -333,6 +335,480 @@ static hipError_t launch_ivf_nch(int nch, int64_t max_items, int cap, int kc, co
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Probe selection (IVFFlatSearch.swift:224-251, smallestIndices :314-382):
+// every centroid's key from its dot with the query in the scalar order of
+// dots.c:40-47 and the host formulas, then the nprobe smallest by (key,
+// index).  The scan does not depend on the probes' order.
+
+// dst[d][c] = src[c][d].
+__global__ __launch_bounds__(256) void ivf_transpose(const float* __restrict__ src, int64_t rows,
+                                                     int dim, float* __restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * dim) return;
+    const int64_t c = i / dim, d = i - c * dim;
+    dst[d * rows + c] = src[i];
+}
+
+constexpr int kCoarseQ = 16;  // queries per block row
+
+// grid (ceil(nlist / 256), ceil(nq / kCoarseQ)); block 256; dynamic LDS
+// (kCoarseQ dim + kCoarseQ) floats.  keys: [nq][nlist].
+__global__ __launch_bounds__(256) void ivf_coarse_keys(const float* __restrict__ queries, int64_t nq,
+                                                       int dim, const float* __restrict__ cent_t,
+                                                       const float* __restrict__ cnorms, int nlist,
+                                                       int metric, float* __restrict__ keys) {
+    extern __shared__ float cq[];
+    float* cqn = cq + kCoarseQ * dim;
+    const int tid = threadIdx.x;
+    const int64_t q0 = (int64_t)blockIdx.y * kCoarseQ;
+    for (int i = tid; i < kCoarseQ * dim; i += blockDim.x) {
+        const int j = i / dim;
+        cq[i] = q0 + j < nq ? queries[(q0 + j) * dim + (i - j * dim)] : 0.0f;
+    }
+    __syncthreads();
+    if (tid < kCoarseQ) {
+        float s = 0.0f;
+        for (int d = 0; d < dim; ++d) s = s + cq[tid * dim + d] * cq[tid * dim + d];
+        cqn[tid] = metric == kMetricIP ? 0.0f : s;
+    }
+    __syncthreads();
+    const int c = blockIdx.x * blockDim.x + tid;
+    if (c >= nlist) return;
+    float acc[kCoarseQ];
+#pragma unroll
+    for (int j = 0; j < kCoarseQ; ++j) acc[j] = 0.0f;
+    for (int d = 0; d < dim; ++d) {
+        const float b = cent_t[(int64_t)d * nlist + c];
+#pragma unroll
+        for (int j = 0; j < kCoarseQ; ++j) acc[j] = acc[j] + cq[j * dim + d] * b;
+    }
+    const float cn = metric == kMetricIP ? 0.0f : cnorms[c];
+#pragma unroll
+    for (int j = 0; j < kCoarseQ; ++j)
+        if (q0 + j < nq) keys[(q0 + j) * nlist + c] = host_distance(acc[j], cqn[j], cn, metric);
+}
+
+constexpr int kProbeLdsSlots = 8192;
+
+// Block per query: the np smallest (key, index) of its nlist keys, written
+// in any order.  dynamic LDS: nlist slots when nlist <= kProbeLdsSlots.
+__global__ __launch_bounds__(256) void ivf_probe_select(const float* __restrict__ keys, int nlist,
+                                                        int np, uint32_t* __restrict__ probes) {
+    extern __shared__ uint64_t lds[];
+    __shared__ uint32_t hist[256];
+    __shared__ int cnt;
+    const int tid = threadIdx.x;
+    const int64_t q = blockIdx.x;
+    const float* kq = keys + q * nlist;
+    const bool in_lds = nlist <= kProbeLdsSlots;
+    if (in_lds)
+        for (int c = tid; c < nlist; c += blockDim.x) lds[c] = pack_slot(kq[c], (uint32_t)c);
+    if (tid == 0) cnt = 0;
+    __syncthreads();
+    auto get = [&](int64_t c) { return in_lds ? lds[c] : pack_slot(kq[c], (uint32_t)c); };
+    uint64_t kth;
+    const uint64_t cut = block_radix_cut(get, nlist, np, hist, &kth);
+    for (int c = tid; c < nlist; c += blockDim.x) {
+        if (get(c) <= cut) {
+            const int p = atomicAdd(&cnt, 1);
+            if (p < np) probes[q * np + p] = (uint32_t)c;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// List-major batch scan (first round of a batch of at least kLmMinBatch
+// queries).  The per-query scan above reads a list once for every query
+// that probes it; here each probed list is read once per batch: the
+// (query, probe) pairs are grouped by list, and a work item takes one chunk
+// of up to kLmRows rows of a list and up to kLmQueries of the queries
+// probing it.  The item stages its queries and, tile by tile, the chunk's
+// rows in LDS (the next tile's loads in flight), forms every (query, row)
+// fast dot with fused multiply-adds in register tiles of one query by
+// several rows (the tile's query width follows the item's query count: 4, 8
+// or 16), turns them into the streaming scan's lower-bound keys and offers
+// each query's keys of the tile to that query's selection (a wave keeps
+// four queries' kc best).  Each (query, chunk) leaves one candidate list.
+// A query's chunk lists hold its kc best keys over all its probed rows (an
+// entry of the kc best has fewer than kc smaller keys in its own chunk), so
+// the per-query merge, exact rescore and proof are those of the per-query
+// scan; queries whose proof fails go back to it with a larger candidate
+// count.
+constexpr int kLmRows = 512;
+constexpr int kLmQueries = 16;
+constexpr int64_t kLmMinBatch = 64;
+constexpr int kLmMaxNch = 4;  // dim <= 256
+
+template <int NCH>
+struct LmShape {
+    static constexpr int kT = NCH <= 2 ? 64 : 32;         // rows per LDS tile
+    static constexpr int kRowF = 64 * NCH + 4;            // floats per staged row
+    static constexpr int kQF = 64 * NCH + 4;              // floats per staged query
+    static constexpr int kLoads = kT * 16 * NCH / 256;    // float4 tile loads per thread
+    static constexpr int kMinGp = NCH <= 2 ? 4 : 8;       // narrowest register tile
+    static constexpr size_t kQsOff = 0;
+    static constexpr size_t kQnOff = kQsOff + sizeof(float) * kLmQueries * kQF;
+    static constexpr size_t kTileOff = kQnOff + sizeof(float) * kLmQueries;
+    static constexpr size_t kVnOff = kTileOff + sizeof(float) * kT * kRowF;
+    static constexpr size_t kKeyOff = kVnOff + sizeof(float) * kT;
+    static constexpr size_t kSelOff = (kKeyOff + sizeof(float) * kLmQueries * kT + 15) / 16 * 16;
+    static constexpr size_t kBytes = kSelOff + sizeof(uint64_t) * kLmQueries * 128;
+};
+
+struct LmArgs {
+    const float* packed;
+    const float* packed_norms;
+    const int64_t* offsets;   // [nlist + 1] packed rows of each list
+    const uint32_t* probes;   // [nq][np]
+    const int32_t* lstart;    // [nlist + 1] first (query, probe) pair of each list
+    const int32_t* lpairs;    // [nq np] pairs q np + p grouped by list
+    const int32_t* item_off;  // [nlist + 1] first work item of each list
+    const int32_t* qchunk;    // [nq][np] the query's first chunk list of probe p
+    const int64_t* qbase;     // [nq + 1] the query's first candidate list
+    int np;
+    int nlist;
+};
+
+// Thread per (query, probe) pair: lcount[list] += 1.
+__global__ __launch_bounds__(256) void ivf_lm_count(const uint32_t* __restrict__ probes,
+                                                    int64_t pairs, int32_t* __restrict__ lcount) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < pairs) atomicAdd(&lcount[probes[i]], 1);
+}
+
+// One block: lstart = exclusive scan of the pair counts, item_off = the
+// exclusive scan of each list's items (chunks x query groups); the counts
+// are zeroed for the fill.
+__global__ __launch_bounds__(1024) void ivf_lm_lists(int32_t* __restrict__ lcount,
+                                                     const int64_t* __restrict__ offsets, int nlist,
+                                                     int32_t* __restrict__ lstart,
+                                                     int32_t* __restrict__ item_off) {
+    __shared__ int32_t part_p[1024], part_i[1024];
+    const int tid = threadIdx.x;
+    const int per = (nlist + 1023) / 1024;
+    const int a = tid * per, b = a + per < nlist ? a + per : nlist;
+    auto items_of = [&](int L, int32_t m) {
+        const int64_t rows = offsets[L + 1] - offsets[L];
+        if (m == 0 || rows == 0) return (int32_t)0;
+        return (int32_t)(((rows + kLmRows - 1) / kLmRows) * ((m + kLmQueries - 1) / kLmQueries));
+    };
+    int32_t sp = 0, si = 0;
+    for (int L = a; L < b; ++L) {
+        sp += lcount[L];
+        si += items_of(L, lcount[L]);
+    }
+    part_p[tid] = sp;
+    part_i[tid] = si;
+    __syncthreads();
+    if (tid == 0) {
+        int32_t rp = 0, ri = 0;
+        for (int t = 0; t < 1024; ++t) {
+            const int32_t vp = part_p[t], vi = part_i[t];
+            part_p[t] = rp;
+            part_i[t] = ri;
+            rp += vp;
+            ri += vi;
+        }
+        lstart[nlist] = rp;
+        item_off[nlist] = ri;
+    }
+    __syncthreads();
+    int32_t rp = part_p[tid], ri = part_i[tid];
+    for (int L = a; L < b; ++L) {
+        const int32_t m = lcount[L];
+        lstart[L] = rp;
+        item_off[L] = ri;
+        rp += m;
+        ri += items_of(L, m);
+        lcount[L] = 0;
+    }
+}
+
+// Thread per pair: its place among its list's pairs (any order).
+__global__ __launch_bounds__(256) void ivf_lm_fill(const uint32_t* __restrict__ probes,
+                                                   int64_t pairs, const int32_t* __restrict__ lstart,
+                                                   int32_t* __restrict__ lfill,
+                                                   int32_t* __restrict__ lpairs) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= pairs) return;
+    const uint32_t L = probes[i];
+    lpairs[lstart[L] + atomicAdd(&lfill[L], 1)] = (int32_t)i;
+}
+
+// Wave per query: the first chunk list of each probe among the query's
+// lists, the query's list count and its probed rows.
+__global__ __launch_bounds__(256) void ivf_lm_qplan(const uint32_t* __restrict__ probes, int np,
+                                                    int64_t nq, const int64_t* __restrict__ offsets,
+                                                    int32_t* __restrict__ qchunk,
+                                                    int32_t* __restrict__ qcount,
+                                                    int64_t* __restrict__ qtotal) {
+    const int lane = threadIdx.x & 63;
+    const int64_t q = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (q >= nq) return;  // the whole wave leaves together
+    int32_t carry = 0;
+    int64_t rows_all = 0;
+    for (int base = 0; base < np; base += 64) {
+        const int p = base + lane;
+        int32_t nch = 0;
+        int64_t rows = 0;
+        if (p < np) {
+            const uint32_t L = probes[q * np + p];
+            rows = offsets[L + 1] - offsets[L];
+            nch = (int32_t)((rows + kLmRows - 1) / kLmRows);
+        }
+        int32_t incl = nch;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int32_t t = __shfl_up(incl, o);
+            if (lane >= o) incl += t;
+        }
+        if (p < np) qchunk[q * np + p] = carry + incl - nch;
+        carry += __shfl(incl, 63);
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) rows += __shfl_xor(rows, o);
+        rows_all += rows;
+    }
+    if (lane == 0) {
+        qcount[q] = carry;
+        qtotal[q] = rows_all;
+    }
+}
+
+// One block: qbase = exclusive scan of the queries' list counts.
+__global__ __launch_bounds__(1024) void ivf_lm_qscan(const int32_t* __restrict__ qcount, int64_t nq,
+                                                     int64_t* __restrict__ qbase) {
+    __shared__ int64_t part[1024];
+    const int tid = threadIdx.x;
+    const int64_t per = (nq + 1023) / 1024;
+    const int64_t a = tid * per, b = a + per < nq ? a + per : nq;
+    int64_t sum = 0;
+    for (int64_t i = a; i < b; ++i) sum += qcount[i];
+    part[tid] = sum;
+    __syncthreads();
+    if (tid == 0) {
+        int64_t run = 0;
+        for (int t = 0; t < 1024; ++t) {
+            const int64_t v = part[t];
+            part[t] = run;
+            run += v;
+        }
+        qbase[nq] = run;
+    }
+    __syncthreads();
+    int64_t run = part[tid];
+    for (int64_t i = a; i < b; ++i) {
+        qbase[i] = run;
+        run += qcount[i];
+    }
+}
+
+// The dots of one tile for GP queries: thread t takes query t % GP and rows
+// t / GP + (256 / GP) j; their keys go to tkeys[query][row].
+template <int NCH, int GP>
+__device__ __forceinline__ void lm_tile_keys(const float* qs, const float* qnorm, const float* tile,
+                                             const float* vn, float* tkeys, int dim4, int nvalid,
+                                             int metric, const BoundCoef& bc) {
+    using S = LmShape<NCH>;
+    constexpr int kStep = 256 / GP, kPer = S::kT / kStep;
+    const int tid = threadIdx.x, gq = tid % GP, rs = tid / GP;
+    float acc[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) acc[j] = 0.0f;
+    const float* qrow = qs + gq * S::kQF;
+    for (int d4 = 0; d4 < dim4; ++d4) {
+        const f4v x = *reinterpret_cast<const f4v*>(qrow + 4 * d4);
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const f4v y = *reinterpret_cast<const f4v*>(tile + (rs + kStep * j) * S::kRowF + 4 * d4);
+            acc[j] = fmaf(x.x, y.x, acc[j]);
+            acc[j] = fmaf(x.y, y.y, acc[j]);
+            acc[j] = fmaf(x.z, y.z, acc[j]);
+            acc[j] = fmaf(x.w, y.w, acc[j]);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int r = rs + kStep * j;
+        if (r < nvalid) tkeys[gq * S::kT + r] = lower_key(acc[j], qnorm[gq], vn[r], metric, bc);
+    }
+}
+
+// Persistent grid over the work items; block 256; dynamic LDS
+// LmShape<NCH>::kBytes.  cand: kc slots per (query, chunk) list.
+template <int NCH>
+__global__ __launch_bounds__(256) void ivf_lm_scan(LmArgs la, int dim,
+                                                   const float* __restrict__ queries, int metric,
+                                                   BoundCoef bc, int kc, uint64_t* __restrict__ cand) {
+    using S = LmShape<NCH>;
+    constexpr int kT = S::kT;
+    extern __shared__ __align__(16) uint8_t lm_lds[];
+    float* qs = reinterpret_cast<float*>(lm_lds + S::kQsOff);
+    float* qnorm = reinterpret_cast<float*>(lm_lds + S::kQnOff);
+    float* tile = reinterpret_cast<float*>(lm_lds + S::kTileOff);
+    float* vn = reinterpret_cast<float*>(lm_lds + S::kVnOff);
+    float* tkeys = reinterpret_cast<float*>(lm_lds + S::kKeyOff);
+    uint64_t* selbuf = reinterpret_cast<uint64_t*>(lm_lds + S::kSelOff);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int dim4 = dim >> 2;
+    const int total_items = la.item_off[la.nlist];
+    for (int item = blockIdx.x; item < total_items; item += gridDim.x) {
+        // The item's list: the last L with item_off[L] <= item.
+        int lo = 0, hi = la.nlist;
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (la.item_off[mid] <= item) lo = mid;
+            else hi = mid;
+        }
+        const int L = lo;
+        const int64_t r0 = la.offsets[L], nrows = la.offsets[L + 1] - r0;
+        const int nchunk = (int)((nrows + kLmRows - 1) / kLmRows);
+        const int li = item - la.item_off[L];
+        const int g = li / nchunk, c = li - g * nchunk;
+        const int p0 = la.lstart[L] + g * kLmQueries;
+        const int mg = min(kLmQueries, la.lstart[L + 1] - p0);
+        const int gp = mg <= S::kMinGp ? S::kMinGp : (mg <= 8 ? 8 : 16);
+        const int64_t a = r0 + (int64_t)c * kLmRows;
+        const int64_t b = a + kLmRows < r0 + nrows ? a + kLmRows : r0 + nrows;
+        __syncthreads();  // the previous item is done with the LDS
+        for (int e = tid; e < kLmQueries * 16 * NCH; e += 256) {
+            const int qq = e / (16 * NCH), d4 = e - qq * 16 * NCH;
+            f4v v = {0.f, 0.f, 0.f, 0.f};
+            if (qq < mg && d4 < dim4) {
+                const int q = la.lpairs[p0 + qq] / la.np;
+                v = *reinterpret_cast<const f4v*>(queries + (int64_t)q * dim + 4 * d4);
+            }
+            *reinterpret_cast<f4v*>(qs + qq * S::kQF + 4 * d4) = v;
+        }
+        __syncthreads();
+        {
+            // Fast query norms: 16 lanes per query.
+            const int qq = wave * 4 + (lane >> 4), lr = lane & 15;
+            float acc = 0.0f;
+            for (int d4 = lr; d4 < 16 * NCH; d4 += 16) {
+                const f4v v = *reinterpret_cast<const f4v*>(qs + qq * S::kQF + 4 * d4);
+                acc = fmaf(v.x, v.x, acc);
+                acc = fmaf(v.y, v.y, acc);
+                acc = fmaf(v.z, v.z, acc);
+                acc = fmaf(v.w, v.w, acc);
+            }
+            acc = row16_sum(acc);
+            if (lr == 0) qnorm[qq] = acc;
+        }
+        // Wave w keeps the selections of queries w, w + 4, w + 8, w + 12.
+        WaveTopKT<128> sel[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sel[i].init(selbuf + (wave + 4 * i) * 128, 128, kc);
+        // Row tiles, the next one's loads in flight during the current one's dots.
+        f4v pf[S::kLoads];
+        float pvn = 0.0f;
+        auto load_tile = [&](int64_t t0) {
+#pragma unroll
+            for (int j = 0; j < S::kLoads; ++j) {
+                const int e = tid + 256 * j;
+                const int r = e / (16 * NCH), d4 = e - r * 16 * NCH;
+                const bool in = t0 + r < b && d4 < dim4;
+                const int64_t row = in ? t0 + r : a;
+                const f4v t = load_stream(la.packed + row * dim + (in ? 4 * d4 : 0));
+                pf[j] = in ? t : f4v{0.f, 0.f, 0.f, 0.f};
+            }
+            pvn = tid < kT && t0 + tid < b ? la.packed_norms[t0 + tid] : 0.0f;
+        };
+        load_tile(a);
+        for (int64_t t0 = a; t0 < b; t0 += kT) {
+            __syncthreads();  // the previous tile's dots are done
+#pragma unroll
+            for (int j = 0; j < S::kLoads; ++j) {
+                const int e = tid + 256 * j;
+                const int r = e / (16 * NCH), d4 = e - r * 16 * NCH;
+                *reinterpret_cast<f4v*>(tile + r * S::kRowF + 4 * d4) = pf[j];
+            }
+            if (tid < kT) vn[tid] = pvn;
+            __syncthreads();
+            if (t0 + kT < b) load_tile(t0 + kT);
+            const int nvalid = b - t0 < kT ? (int)(b - t0) : kT;
+            if (gp == 16) lm_tile_keys<NCH, 16>(qs, qnorm, tile, vn, tkeys, dim4, nvalid, metric, bc);
+            else if (gp == 8) lm_tile_keys<NCH, 8>(qs, qnorm, tile, vn, tkeys, dim4, nvalid, metric, bc);
+            else lm_tile_keys<NCH, S::kMinGp>(qs, qnorm, tile, vn, tkeys, dim4, nvalid, metric, bc);
+            __syncthreads();  // the tile's keys are in tkeys
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int qq = wave + 4 * i;
+                if (qq < mg) {
+                    const bool v = lane < nvalid;
+                    sel[i].offer(v, v ? tkeys[qq * kT + lane] : 0.0f, (uint32_t)(t0 + lane));
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int qq = wave + 4 * i;
+            if (qq >= mg) continue;
+            sel[i].finish();
+            const int pair = la.lpairs[p0 + qq];
+            const int q = pair / la.np, pr = pair - q * la.np;
+            uint64_t* dst = cand + (la.qbase[q] + la.qchunk[(int64_t)q * la.np + pr] + c) * (int64_t)kc;
+            for (int sidx = lane; sidx < kc; sidx += 64)
+                dst[sidx] = sidx < sel[i].count ? sel[i].buf[sidx] : kEmptySlot;
+        }
+    }
+}
+
+// Block per query: the kc best of its chunk lists, exact rescore (list ids
+// reported), proof.  dynamic LDS: 4 * cap slots.
+template <int NCH>
+__global__ __launch_bounds__(256) void ivf_lm_merge(LmArgs la, const int64_t* __restrict__ qtotal,
+                                                    int dim, const float* __restrict__ queries,
+                                                    const uint32_t* __restrict__ list_ids,
+                                                    int metric, int kc, int cap,
+                                                    const uint64_t* __restrict__ cand, FlatArgs fa) {
+    extern __shared__ uint64_t lds[];
+    const int lane = threadIdx.x & 63, lr = lane & 15;
+    const uint32_t q = blockIdx.x;
+    const int dim4 = dim >> 2;
+    const float* qp = queries + (int64_t)q * dim;
+    f4v qv[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const int idx = lr + 16 * c;
+        qv[c] = idx < dim4 ? *reinterpret_cast<const f4v*>(qp + 4 * idx) : f4v{0.f, 0.f, 0.f, 0.f};
+    }
+    const int64_t first = la.qbase[q], nlists = la.qbase[q + 1] - first;
+    WaveTopK sel;
+    block_select_lists(cand + first * kc, nlists * kc, lds, cap, kc, sel);
+    final_rescore_f4<NCH>(qv, la.packed, la.packed_norms, qtotal[q], dim, metric, q, lds, kc, fa,
+                          kFltMax, kProofFlat, list_ids, (int)q);
+}
+
+template <int NCH>
+static hipError_t launch_lm(const LmArgs& la, const int64_t* qtotal, int64_t nq, int dim,
+                            const float* queries, const uint32_t* list_ids, int metric,
+                            const BoundCoef& bc, int kc, uint64_t* cand, const FlatArgs& fa,
+                            hipStream_t st) {
+    using S = LmShape<NCH>;
+    static const bool attr = [] {
+        (void)hipFuncSetAttribute((const void*)ivf_lm_scan<NCH>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::kBytes);
+        return true;
+    }();
+    (void)attr;
+    hipLaunchKernelGGL(ivf_lm_scan<NCH>, dim3(1024), dim3(256), S::kBytes, st, la, dim, queries,
+                       metric, bc, kc, cand);
+    const int cap = flat_cap_for(kc);
+    hipLaunchKernelGGL(ivf_lm_merge<NCH>, dim3((unsigned)nq), dim3(256),
+                       sizeof(uint64_t) * 4 * (size_t)cap, st, la, qtotal, dim, queries, list_ids,
+                       metric, kc, cap, (const uint64_t*)cand, fa);
+    return hipGetLastError();
+}
+
+static bool ivf_list_major_enabled() {
+    static const bool on = [] {
+        const char* e = std::getenv("MANS_IVF_LIST_MAJOR");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+
 constexpr int kIvfMaxDim = 512;
 
 // Queries and outputs in device memory.  h_probes (nullable, host): nq x np
@@ -356,12 +832,25 @@ static int ivf_search_run(mans_ctx* ctx, const mans_ivf* ivf, const float* d_q, 
 
     // Probes: the np nearest centroids by (distance, index).  The scan does
     // not depend on their order; the reported probe lists are ascending.
-    hipError_t e = slot->aux0.ensure((size_t)nq * np * sizeof(float), ctx->fail_alloc);
+    const int nlist_i = (int)ivf->nlist;
+    const int64_t pchunk = std::min<int64_t>(nq, 2048);  // queries per key pass
+    hipError_t e = slot->aux0.ensure((size_t)pchunk * nlist_i * sizeof(float), ctx->fail_alloc);
     if (e == hipSuccess) e = slot->aux1.ensure((size_t)nq * np * sizeof(uint32_t), ctx->fail_alloc);
     if (e != hipSuccess) return hip_fail(e, "IVF probe workspace");
-    int rc = flat_search_run(ctx, ivf->cent, d_q, nq, np, metric, (float*)slot->aux0.p,
-                             (uint32_t*)slot->aux1.p, st, slot, nullptr, nullptr);
-    if (rc != MANS_OK) return rc;
+    ctx->time_begin(slot, st);
+    for (int64_t q0 = 0; q0 < nq && e == hipSuccess; q0 += pchunk) {
+        const int64_t m = std::min<int64_t>(pchunk, nq - q0);
+        const dim3 grid((unsigned)((nlist_i + 255) / 256), (unsigned)((m + kCoarseQ - 1) / kCoarseQ));
+        hipLaunchKernelGGL(ivf_coarse_keys, grid, dim3(256), sizeof(float) * (kCoarseQ * dim + kCoarseQ),
+                           st, d_q + q0 * dim, m, dim, (const float*)ivf->cent_t.p,
+                           (const float*)ivf->cent->norms.p, nlist_i, (int)metric, (float*)slot->aux0.p);
+        hipLaunchKernelGGL(ivf_probe_select, dim3((unsigned)m), dim3(256),
+                           nlist_i <= kProbeLdsSlots ? sizeof(uint64_t) * nlist_i : 0, st,
+                           (const float*)slot->aux0.p, nlist_i, np, (uint32_t*)slot->aux1.p + q0 * np);
+        e = hipGetLastError();
+    }
+    ctx->time_end(slot, st, "ivf_probe");
+    if (e != hipSuccess) return hip_fail(e, "IVF probes");
     const uint32_t* d_probes = (const uint32_t*)slot->aux1.p;
     if (h_probes) {
         std::vector<uint32_t> pr((size_t)nq * np);
@@ -398,6 +887,92 @@ static int ivf_search_run(mans_ctx* ctx, const mans_ivf* ivf, const float* d_q, 
     std::vector<uint32_t> pending;
     int64_t npend = nq;
     ctx->time_begin(slot, st);
+    if (nq >= kLmMinBatch && nch <= kLmMaxNch && kc <= 64 && ivf_list_major_enabled()) {
+        // First round list-major; the queries whose proof fails continue
+        // below with a larger candidate count.
+        const int nlist = (int)ivf->nlist;
+        const int64_t pairs = nq * np;
+        const int64_t lists_bound = nq * ((int64_t)np + max_rows / kLmRows + 1);
+        size_t off = 0;
+        auto take = [&](size_t bytes) {
+            const size_t at = off;
+            off += (bytes + 15) / 16 * 16;
+            return at;
+        };
+        const size_t o_lcount = take((size_t)nlist * 4), o_lstart = take((size_t)(nlist + 1) * 4);
+        const size_t o_item = take((size_t)(nlist + 1) * 4), o_pairs = take((size_t)pairs * 4);
+        const size_t o_qchunk = take((size_t)pairs * 4), o_qcount = take((size_t)nq * 4);
+        const size_t o_qbase = take((size_t)(nq + 1) * 8), o_qtotal = take((size_t)nq * 8);
+        e = slot->aux2.ensure(off, ctx->fail_alloc);
+        if (e == hipSuccess)
+            e = slot->cand.ensure((size_t)lists_bound * kc * sizeof(uint64_t), ctx->fail_alloc);
+        if (e == hipSuccess) e = slot->status_h.ensure((size_t)nq);
+        if (e != hipSuccess) return hip_fail(e, "IVF list-major workspace");
+        char* base = (char*)slot->aux2.p;
+        int32_t* lcount = (int32_t*)(base + o_lcount);
+        LmArgs la;
+        la.packed = (const float*)ivf->packed.p;
+        la.packed_norms = (const float*)ivf->packed_norms.p;
+        la.offsets = (const int64_t*)ivf->offsets.p;
+        la.probes = d_probes;
+        la.lstart = (const int32_t*)(base + o_lstart);
+        la.lpairs = (const int32_t*)(base + o_pairs);
+        la.item_off = (const int32_t*)(base + o_item);
+        la.qchunk = (const int32_t*)(base + o_qchunk);
+        la.qbase = (const int64_t*)(base + o_qbase);
+        la.np = np;
+        la.nlist = nlist;
+        const int64_t* qtotal = (const int64_t*)(base + o_qtotal);
+        e = hipMemsetAsync(lcount, 0, (size_t)nlist * 4, st);
+        const unsigned pblocks = (unsigned)((pairs + 255) / 256);
+        if (e == hipSuccess) {
+            hipLaunchKernelGGL(ivf_lm_count, dim3(pblocks), dim3(256), 0, st, d_probes, pairs, lcount);
+            hipLaunchKernelGGL(ivf_lm_lists, dim3(1), dim3(1024), 0, st, lcount,
+                               (const int64_t*)ivf->offsets.p, nlist, (int32_t*)la.lstart,
+                               (int32_t*)la.item_off);
+            hipLaunchKernelGGL(ivf_lm_fill, dim3(pblocks), dim3(256), 0, st, d_probes, pairs,
+                               la.lstart, lcount, (int32_t*)la.lpairs);
+            hipLaunchKernelGGL(ivf_lm_qplan, dim3((unsigned)((nq + 3) / 4)), dim3(256), 0, st,
+                               d_probes, np, nq, (const int64_t*)ivf->offsets.p,
+                               (int32_t*)la.qchunk, (int32_t*)(base + o_qcount),
+                               (int64_t*)qtotal);
+            hipLaunchKernelGGL(ivf_lm_qscan, dim3(1), dim3(1024), 0, st,
+                               (const int32_t*)(base + o_qcount), nq, (int64_t*)la.qbase);
+            e = hipGetLastError();
+        }
+        FlatArgs fa = {};
+        fa.out_dist = d_dist;
+        fa.out_ids = d_ids;
+        fa.status = (uint8_t*)slot->status_h.p;  // pinned: read after the stream syncs
+        fa.k = keff;
+        fa.k_stride = (int)k;
+        const BoundCoef bc = make_bounds(dim);
+        uint64_t* cand = (uint64_t*)slot->cand.p;
+        const float* lq = d_q;
+        const uint32_t* lids = (const uint32_t*)ivf->list_ids.p;
+        ctx->time_begin(slot, st);
+        if (e == hipSuccess) {
+            switch (nch) {
+            case 1: e = launch_lm<1>(la, qtotal, nq, dim, lq, lids, (int)metric, bc, kc, cand, fa, st); break;
+            case 2: e = launch_lm<2>(la, qtotal, nq, dim, lq, lids, (int)metric, bc, kc, cand, fa, st); break;
+            case 3: e = launch_lm<3>(la, qtotal, nq, dim, lq, lids, (int)metric, bc, kc, cand, fa, st); break;
+            default: e = launch_lm<4>(la, qtotal, nq, dim, lq, lids, (int)metric, bc, kc, cand, fa, st); break;
+            }
+        }
+        ctx->time_end(slot, st, "ivf_lm");
+        if (e == hipSuccess) e = hipStreamSynchronize(st);
+        if (e != hipSuccess) return hip_fail(e, "IVF list-major scan");
+        const uint8_t* sh = (const uint8_t*)slot->status_h.p;
+        for (int64_t i = 0; i < nq; ++i)
+            if (sh[i]) pending.push_back((uint32_t)i);
+        if (pending.empty()) {
+            ctx->time_end(slot, st, "ivf_scan");
+            return MANS_OK;
+        }
+        npend = (int64_t)pending.size();
+        kc *= 4;
+        ctx->proof_retries += npend;
+    }
     for (;;) {
         if (exact) {
             kc = 32;
@@ -524,6 +1099,14 @@ static int ivf_build_from_centroids(mans_ctx* ctx, const mans_corpus* corpus, ma
                            hipMemcpyHostToDevice, st);
     if (e == hipSuccess && n > 0)
         e = hipMemcpyAsync(ivf->list_ids.p, list_ids.data(), n * sizeof(uint32_t), hipMemcpyHostToDevice, st);
+    if (e == hipSuccess)
+        e = ivf->cent_t.ensure((size_t)ivf->nlist * dim * sizeof(float), ctx->fail_alloc);
+    if (e == hipSuccess && ivf->nlist > 0) {
+        const int64_t cells = ivf->nlist * dim;
+        hipLaunchKernelGGL(ivf_transpose, dim3((unsigned)((cells + 255) / 256)), dim3(256), 0, st,
+                           (const float*)cent->rows.p, ivf->nlist, (int)dim, (float*)ivf->cent_t.p);
+        e = hipGetLastError();
+    }
     if (e == hipSuccess && n > 0) {
         hipLaunchKernelGGL(ivf_gather_rows, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st,
                            (const float*)corpus->rows.p, (const float*)corpus->norms.p,

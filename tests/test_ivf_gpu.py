@@ -56,6 +56,33 @@ def test_ivf_lists_probes_and_results_match_oracle(gpu_ctx, metric):
     c.release()
 
 
+@pytest.mark.parametrize("dim", [64, 100, 128, 192, 256])
+def test_ivf_list_major_batch_matches_oracle(gpu_ctx, dim):
+    # Batches of 64 queries and more scan each probed list once for all the
+    # queries probing it (chunks of 512 rows, 16 queries per work item);
+    # results must equal the oracle's per-query scan exactly, for every
+    # metric, with lists larger than a chunk, k up to 32 and some queries
+    # whose probes reach only empty lists.
+    n, nlist, nq = 9000, 12, 80
+    rows = workloads.lcg_vectors(1, n, dim, seed=640 + dim)
+    cents = np.concatenate([rows[:nlist - 2], np.full((2, dim), 1e3, np.float32)])
+    queries = workloads.lcg_vectors(1, nq, dim, seed=641 + dim)
+    queries[5] = 1e3  # nearest centroids: the two empty lists
+    for metric in (L2, COS, IP):
+        part = oracle.IVFPartition(rows, cents, metric)
+        c = gpu_ctx.upload(rows)
+        ivf = c.ivf_flat_build(cents, metric)
+        for nprobe, k in ((1, 10), (2, 1), (5, 32), (12, 10)):
+            print(f"ivf list-major dim{dim} m{metric} nprobe{nprobe} k{k}", flush=True)
+            gd, gi, gp = ivf.search(queries, k, nprobe, want_probes=True)
+            for qi in range(nq):
+                od, oi, op = part.search(queries[qi], k, nprobe)
+                assert np.array_equal(gp[qi], op), f"probes q{qi}"
+                _assert_rows(gd[qi], gi[qi], od, oi, f"lm dim{dim} m{metric} np{nprobe} k{k} q{qi}")
+        ivf.release()
+        c.release()
+
+
 def test_ivf_full_probe_equals_flat(gpu_ctx):
     dim, n, nlist = 128, 5000, 20
     rows = workloads.lcg_vectors(0, n, dim, seed=611)
