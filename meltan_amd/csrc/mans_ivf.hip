@@ -452,7 +452,9 @@ struct LmShape {
     static constexpr size_t kTileOff = kQnOff + sizeof(float) * kLmQueries;
     static constexpr size_t kVnOff = kTileOff + sizeof(float) * kT * kRowF;
     static constexpr size_t kKeyOff = kVnOff + sizeof(float) * kT;
-    static constexpr size_t kSelOff = (kKeyOff + sizeof(float) * kLmQueries * kT + 15) / 16 * 16;
+    static constexpr int kKeyStride = kT + 1;             // keys per query, padded (banks)
+    static constexpr size_t kSelOff =
+        (kKeyOff + sizeof(float) * kLmQueries * kKeyStride + 15) / 16 * 16;
     static constexpr size_t kBytes = kSelOff + sizeof(uint64_t) * kLmQueries * 128;
 };
 
@@ -630,7 +632,7 @@ __device__ __forceinline__ void lm_tile_keys(const float* qs, const float* qnorm
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
         const int r = rs + kStep * j;
-        if (r < nvalid) tkeys[gq * S::kT + r] = lower_key(acc[j], qnorm[gq], vn[r], metric, bc);
+        if (r < nvalid) tkeys[gq * S::kKeyStride + r] = lower_key(acc[j], qnorm[gq], vn[r], metric, bc);
     }
 }
 
@@ -736,7 +738,7 @@ __global__ __launch_bounds__(256) void ivf_lm_scan(LmArgs la, int dim,
                 const int qq = wave + 4 * i;
                 if (qq < mg) {
                     const bool v = lane < nvalid;
-                    sel[i].offer(v, v ? tkeys[qq * kT + lane] : 0.0f, (uint32_t)(t0 + lane));
+                    sel[i].offer(v, v ? tkeys[qq * S::kKeyStride + lane] : 0.0f, (uint32_t)(t0 + lane));
                 }
             }
         }
