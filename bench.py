@@ -381,6 +381,80 @@ def bench_single_queries(args, ctx, which):
 
 
 # ---------------------------------------------------------------------------
+# Tier crossover (FlatGPUSearch.swift:31-95, BENCHMARKS.md:193-199)
+# ---------------------------------------------------------------------------
+
+def bench_tiers(args, ctx):
+    """Single-query latency of the four flat tiers across corpus sizes at
+    dim 384, k 24, cosine (the reference's crossover measurement): the
+    device fp32 scan and the device int8 bounded scan (mode 0) through the
+    host-pointer C ABI (query upload and results back included), and the
+    host fp32 ParallelFlatScan and host int8 BoundedExactScan restated in
+    the oracle (the CPU baselines of those tiers, 16 host threads).  p50 by
+    nearest rank; the crossovers are where one tier's p50 drops below
+    another's."""
+    import meltan_amd as M
+    from meltan_amd import workloads
+    from oracle import oracle
+
+    dim, k, metric = 384, 24, M.METRIC_COSINE
+    sizes = [128, 256, 512, 1024, 4096, 16384, 20480, 24576, 32768, 50000, 100000, 262144,
+             400000, 600000, 800000, 1000000]
+    log("tiers: generating 1,000,000 x 384 N(0,1) normalised rows (prefixes per size)")
+    db_all = workloads.gauss_rows(1001, sizes[-1], dim, True)
+    q = workloads.gauss_rows(1002, 64, dim, True)
+    rows = []
+    for n in sizes:
+        db = db_all[:n]
+        c = ctx.upload(db)
+        norms = oracle.row_norms(db)
+
+        def p50(fn, reps):
+            lat = []
+            for i in range(reps):
+                t = time.perf_counter()
+                fn(i % q.shape[0])
+                lat.append((time.perf_counter() - t) * 1e6)
+            return round(percentile_nearest_rank(lat, 0.5), 2)
+
+        for i in range(20):
+            c.flat_search(q[i:i + 1], k, metric)
+        row = {"n": n, "gpu_fp32_us": p50(lambda i: c.flat_search(q[i:i + 1], k, metric), 300)}
+        if n >= 16384:
+            for i in range(10):
+                c.int8_search(q[i:i + 1], k, metric, mode=0)
+            row["gpu_int8_us"] = p50(lambda i: c.int8_search(q[i:i + 1], k, metric, mode=0), 200)
+        if not args.no_cpu:
+            slices = max(1, min(CPU_THREADS, 32, n // 2048))
+            row["host_fp32_us"] = p50(lambda i: oracle.flat_search(
+                db, norms, q[i], k, metric, cores=CPU_THREADS, threads=slices),
+                40 if n <= 100000 else 10)
+            row["host_fp32_threads"] = slices
+            if n >= 16384:
+                planes = oracle.int8_build(db)
+                row["host_int8_us"] = p50(lambda i: oracle.int8_search(
+                    db, norms, planes, q[i], k, metric, cores=CPU_THREADS, mode=0),
+                    20 if n <= 100000 else 4)
+                del planes
+        rows.append(row)
+        log(f"tiers: n {n}: " + ", ".join(f"{a} {b}" for a, b in row.items() if a != "n"))
+        c.release()
+
+    def first(pred):
+        for r in rows:
+            if pred(r):
+                return r["n"]
+        return None
+
+    cross = {"gpu_fp32_below_host_fp32_from_n": first(
+        lambda r: "host_fp32_us" in r and r["gpu_fp32_us"] < r["host_fp32_us"]),
+        "gpu_int8_below_gpu_fp32_from_n": first(
+        lambda r: "gpu_int8_us" in r and r["gpu_int8_us"] < r["gpu_fp32_us"])}
+    return {"workload": f"single-query tiers, exact top-{k} cosine, dim {dim}, N(0,1) rows",
+            "rows": rows, "crossover": cross}
+
+
+# ---------------------------------------------------------------------------
 # int8 prefilter + fp32 rerank (C3)
 # ---------------------------------------------------------------------------
 
@@ -661,7 +735,7 @@ def main():
     ap.add_argument("--pq-n", type=int, default=10_000_000)
     ap.add_argument("--pq-iters", type=int, default=20,
                     help="IVF-PQ training iterations (IVFPQConfiguration's default is 20)")
-    ap.add_argument("--workload", default="flat", choices=["flat", "int8", "ivf", "ivfpq"])
+    ap.add_argument("--workload", default="flat", choices=["flat", "int8", "ivf", "ivfpq", "tiers"])
     ap.add_argument("--quick", action="store_true", help="flat only, no 100k or per-config extras")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-queries", type=int, default=128)
@@ -698,7 +772,8 @@ def main():
                 except Exception as exc:  # a failed extra must not hide the main line
                     out[name] = {"error": f"{type(exc).__name__}: {exc}"}
     else:
-        fn = {"int8": bench_int8, "ivf": bench_ivf, "ivfpq": bench_ivfpq}[args.workload]
+        fn = {"int8": bench_int8, "ivf": bench_ivf, "ivfpq": bench_ivfpq,
+              "tiers": bench_tiers}[args.workload]
         out = {"metric": METRIC, "workload": args.workload}
         out.update(fn(args, ctx))
     print(json.dumps(out), flush=True)

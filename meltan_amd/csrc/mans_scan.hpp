@@ -365,7 +365,7 @@ __device__ __forceinline__ void flat_fast_merge_lists(uint64_t* lds, int cap, in
     while (size < nc) size <<= 1;
     for (int i = nc + tid; i < size; i += 256) lds[i] = kEmptySlot;
     __syncthreads();
-    if (wave == 0) wave_bitonic_sort<128>(lds, size);
+    if (wave == 0) wave_bitonic_sort<512>(lds, size);  // up to kFastCandCap slots in registers
     __syncthreads();
 }
 
