@@ -425,9 +425,10 @@ __global__ __launch_bounds__(256) void ivf_probe_select(const float* __restrict_
 // of up to kLmRows rows of a list and up to kLmQueries of the queries
 // probing it.  The item stages its queries and, tile by tile, the chunk's
 // rows in LDS (the next tile's loads in flight), forms every (query, row)
-// fast dot with fused multiply-adds in register tiles of one query by
-// several rows (the tile's query width follows the item's query count: 4, 8
-// or 16), turns them into the streaming scan's lower-bound keys and offers
+// fast dot -- on fp32 MFMA for dim <= 128, else with fused multiply-adds in
+// register tiles of one query by several rows (the tile's query width
+// follows the item's query count: 4, 8 or 16) -- turns them into the
+// streaming scan's lower-bound keys and offers
 // each query's keys of the tile to that query's selection (a wave keeps
 // four queries' kc best).  Each (query, chunk) leaves one candidate list.
 // A query's chunk lists hold its kc best keys over all its probed rows (an
@@ -636,12 +637,51 @@ __device__ __forceinline__ void lm_tile_keys(const float* qs, const float* qnorm
     }
 }
 
+// The dots of one 64-row tile on fp32 MFMA (dim <= 128): wave w takes tile
+// rows 16 w .. 16 w + 15 against all 16 queries with
+// v_mfma_f32_16x16x4f32 (lane l: query l % 16 in A, row l % 16 in B, dims
+// g 16 NCH + s of lane group g = l / 16 at step s: any order of the d
+// products is within the keys' bound); lane l gets (query 4 g + r, row
+// l % 16) for r < 4.  qa: the lane's query values (16 NCH, loaded once per
+// item).  abs_slack covers products and sums the MFMA flushes below
+// 2^-126.
+template <int NCH>
+__device__ __forceinline__ void lm_tile_keys_mfma(const float (&qa)[16 * NCH], const float* qnorm,
+                                                  const float* tile, const float* vn, float* tkeys,
+                                                  int nvalid, int metric, const BoundCoef& bc,
+                                                  float abs_slack) {
+    using S = LmShape<NCH>;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int j = lane & 15, g = lane >> 4;
+    const float* brow = tile + (16 * wave + j) * S::kRowF + g * 16 * NCH;
+    f4v c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < 4 * NCH; ++t) {
+        const f4v b = *reinterpret_cast<const f4v*>(brow + 4 * t);
+        c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[4 * t + 0], b.x, c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[4 * t + 1], b.y, c1, 0, 0, 0);
+        c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[4 * t + 2], b.z, c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[4 * t + 3], b.w, c1, 0, 0, 0);
+    }
+    const int row = 16 * wave + j;
+    if (row < nvalid) {
+        const float v = vn[row];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int q = 4 * g + r;
+            tkeys[q * S::kKeyStride + row] =
+                lower_key(c0[r] + c1[r], qnorm[q], v, metric, bc) - abs_slack;
+        }
+    }
+}
+
 // Persistent grid over the work items; block 256; dynamic LDS
 // LmShape<NCH>::kBytes.  cand: kc slots per (query, chunk) list.
 template <int NCH>
 __global__ __launch_bounds__(256) void ivf_lm_scan(LmArgs la, int dim,
                                                    const float* __restrict__ queries, int metric,
-                                                   BoundCoef bc, int kc, uint64_t* __restrict__ cand) {
+                                                   BoundCoef bc, float abs_slack, int kc,
+                                                   uint64_t* __restrict__ cand) {
     using S = LmShape<NCH>;
     constexpr int kT = S::kT;
     extern __shared__ __align__(16) uint8_t lm_lds[];
@@ -697,6 +737,19 @@ __global__ __launch_bounds__(256) void ivf_lm_scan(LmArgs la, int dim,
             acc = row16_sum(acc);
             if (lr == 0) qnorm[qq] = acc;
         }
+        // The MFMA path's A fragment: query lane % 16, dims g 16 NCH + s.
+        float qa[16 * NCH];
+        if constexpr (NCH <= 2) {
+            const float* qsrc = qs + (lane & 15) * S::kQF + (lane >> 4) * 16 * NCH;
+#pragma unroll
+            for (int t = 0; t < 4 * NCH; ++t) {
+                const f4v v = *reinterpret_cast<const f4v*>(qsrc + 4 * t);
+                qa[4 * t + 0] = v.x;
+                qa[4 * t + 1] = v.y;
+                qa[4 * t + 2] = v.z;
+                qa[4 * t + 3] = v.w;
+            }
+        }
         // Wave w keeps the selections of queries w, w + 4, w + 8, w + 12.
         WaveTopKT<128> sel[4];
 #pragma unroll
@@ -729,9 +782,13 @@ __global__ __launch_bounds__(256) void ivf_lm_scan(LmArgs la, int dim,
             __syncthreads();
             if (t0 + kT < b) load_tile(t0 + kT);
             const int nvalid = b - t0 < kT ? (int)(b - t0) : kT;
-            if (gp == 16) lm_tile_keys<NCH, 16>(qs, qnorm, tile, vn, tkeys, dim4, nvalid, metric, bc);
-            else if (gp == 8) lm_tile_keys<NCH, 8>(qs, qnorm, tile, vn, tkeys, dim4, nvalid, metric, bc);
-            else lm_tile_keys<NCH, S::kMinGp>(qs, qnorm, tile, vn, tkeys, dim4, nvalid, metric, bc);
+            if constexpr (NCH <= 2) {
+                lm_tile_keys_mfma<NCH>(qa, qnorm, tile, vn, tkeys, nvalid, metric, bc, abs_slack);
+            } else {
+                if (gp == 16) lm_tile_keys<NCH, 16>(qs, qnorm, tile, vn, tkeys, dim4, nvalid, metric, bc);
+                else if (gp == 8) lm_tile_keys<NCH, 8>(qs, qnorm, tile, vn, tkeys, dim4, nvalid, metric, bc);
+                else lm_tile_keys<NCH, S::kMinGp>(qs, qnorm, tile, vn, tkeys, dim4, nvalid, metric, bc);
+            }
             __syncthreads();  // the tile's keys are in tkeys
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -794,8 +851,11 @@ static hipError_t launch_lm(const LmArgs& la, const int64_t* qtotal, int64_t nq,
         return true;
     }();
     (void)attr;
+    // Products and partial sums the MFMA flushes below 2^-126 lose at most
+    // 2^-126 each: 2 dim such terms in a dot, counted twice for L2's -2 dot.
+    const float abs_slack = (float)(4.0 * dim * 1.1754943508222875e-38);
     hipLaunchKernelGGL(ivf_lm_scan<NCH>, dim3(1024), dim3(256), S::kBytes, st, la, dim, queries,
-                       metric, bc, kc, cand);
+                       metric, bc, abs_slack, kc, cand);
     const int cap = flat_cap_for(kc);
     hipLaunchKernelGGL(ivf_lm_merge<NCH>, dim3((unsigned)nq), dim3(256),
                        sizeof(uint64_t) * 4 * (size_t)cap, st, la, qtotal, dim, queries, list_ids,
