@@ -467,6 +467,7 @@ struct LmArgs {
     const int32_t* lstart;    // [nlist + 1] first (query, probe) pair of each list
     const int32_t* lpairs;    // [nq np] pairs q np + p grouped by list
     const int32_t* item_off;  // [nlist + 1] first work item of each list
+    const int2* items;        // [items] (list, chunk + group << 16) of each work item
     const int32_t* qchunk;    // [nq][np] the query's first chunk list of probe p
     const int64_t* qbase;     // [nq + 1] the query's first candidate list
     int np;
@@ -525,6 +526,23 @@ __global__ __launch_bounds__(1024) void ivf_lm_lists(int32_t* __restrict__ lcoun
         rp += m;
         ri += items_of(L, m);
         lcount[L] = 0;
+    }
+}
+
+// Thread per list: the descriptors of its work items (chunk-major within a
+// query group: item g nchunk + c).
+__global__ __launch_bounds__(256) void ivf_lm_items(const int32_t* __restrict__ item_off,
+                                                    const int64_t* __restrict__ offsets, int nlist,
+                                                    int2* __restrict__ items) {
+    const int L = blockIdx.x * 256 + threadIdx.x;
+    if (L >= nlist) return;
+    const int first = item_off[L], count = item_off[L + 1] - first;
+    if (count == 0) return;
+    const int64_t rows = offsets[L + 1] - offsets[L];
+    const int nchunk = (int)((rows + kLmRows - 1) / kLmRows);
+    for (int li = 0; li < count; ++li) {
+        const int g = li / nchunk, c = li - g * nchunk;
+        items[first + li] = make_int2(L, c | (g << 16));
     }
 }
 
@@ -695,18 +713,9 @@ __global__ __launch_bounds__(256) void ivf_lm_scan(LmArgs la, int dim,
     const int dim4 = dim >> 2;
     const int total_items = la.item_off[la.nlist];
     for (int item = blockIdx.x; item < total_items; item += gridDim.x) {
-        // The item's list: the last L with item_off[L] <= item.
-        int lo = 0, hi = la.nlist;
-        while (hi - lo > 1) {
-            const int mid = (lo + hi) >> 1;
-            if (la.item_off[mid] <= item) lo = mid;
-            else hi = mid;
-        }
-        const int L = lo;
+        const int2 desc = la.items[item];
+        const int L = desc.x, c = desc.y & 0xFFFF, g = desc.y >> 16;
         const int64_t r0 = la.offsets[L], nrows = la.offsets[L + 1] - r0;
-        const int nchunk = (int)((nrows + kLmRows - 1) / kLmRows);
-        const int li = item - la.item_off[L];
-        const int g = li / nchunk, c = li - g * nchunk;
         const int p0 = la.lstart[L] + g * kLmQueries;
         const int mg = min(kLmQueries, la.lstart[L + 1] - p0);
         const int gp = mg <= S::kMinGp ? S::kMinGp : (mg <= 8 ? 8 : 16);
@@ -965,6 +974,10 @@ static int ivf_search_run(mans_ctx* ctx, const mans_ivf* ivf, const float* d_q, 
         const size_t o_item = take((size_t)(nlist + 1) * 4), o_pairs = take((size_t)pairs * 4);
         const size_t o_qchunk = take((size_t)pairs * 4), o_qcount = take((size_t)nq * 4);
         const size_t o_qbase = take((size_t)(nq + 1) * 8), o_qtotal = take((size_t)nq * 8);
+        // Work items: at most one per (query, chunk of a probed list) plus
+        // one per (list, chunk) for the partial query groups.
+        const int64_t items_bound = lists_bound + ivf->n / kLmRows + nlist;
+        const size_t o_items = take((size_t)items_bound * sizeof(int2));
         e = slot->aux2.ensure(off, ctx->fail_alloc);
         if (e == hipSuccess)
             e = slot->cand.ensure((size_t)lists_bound * kc * sizeof(uint64_t), ctx->fail_alloc);
@@ -980,6 +993,7 @@ static int ivf_search_run(mans_ctx* ctx, const mans_ivf* ivf, const float* d_q, 
         la.lstart = (const int32_t*)(base + o_lstart);
         la.lpairs = (const int32_t*)(base + o_pairs);
         la.item_off = (const int32_t*)(base + o_item);
+        la.items = (const int2*)(base + o_items);
         la.qchunk = (const int32_t*)(base + o_qchunk);
         la.qbase = (const int64_t*)(base + o_qbase);
         la.np = np;
@@ -994,6 +1008,8 @@ static int ivf_search_run(mans_ctx* ctx, const mans_ivf* ivf, const float* d_q, 
                                (int32_t*)la.item_off);
             hipLaunchKernelGGL(ivf_lm_fill, dim3(pblocks), dim3(256), 0, st, d_probes, pairs,
                                la.lstart, lcount, (int32_t*)la.lpairs);
+            hipLaunchKernelGGL(ivf_lm_items, dim3((unsigned)((nlist + 255) / 256)), dim3(256), 0, st,
+                               la.item_off, (const int64_t*)ivf->offsets.p, nlist, (int2*)la.items);
             hipLaunchKernelGGL(ivf_lm_qplan, dim3((unsigned)((nq + 3) / 4)), dim3(256), 0, st,
                                d_probes, np, nq, (const int64_t*)ivf->offsets.p,
                                (int32_t*)la.qchunk, (int32_t*)(base + o_qcount),
