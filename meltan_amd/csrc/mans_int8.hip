@@ -681,6 +681,13 @@ struct I8GemmArgs {
     int64_t seg_rows;         // rows scanned from each segment's start (<= rows_per_seg)
     const uint64_t* qbound;   // nullable, per query: no slot above it is ever needed
     uint64_t* lists;          // [nq][nseg][2][kI8List]
+    // Collect mode of the bounded launch (ccap > 0): every slot at or below
+    // the query's bound is appended to its lane's region instead of the
+    // lane list; a region that overflows sets cflag[query].
+    uint64_t* cbuf = nullptr;     // [nq][nseg][2][ccap]
+    int32_t* ccount = nullptr;    // [nq][nseg][2]
+    uint32_t* cflag = nullptr;    // [nq]
+    int ccap = 0;
 };
 
 // KS 32-byte k-steps per row: the code stride is 32 KS or 32 KS - 16 (the
@@ -717,7 +724,7 @@ __device__ __forceinline__ void lane_list_insert(uint64_t (&l)[C], uint64_t s) {
 // blocks of one segment share b % 8, which places them on one XCD, so the
 // segment's codes are read from HBM once into that XCD's L2.
 // BOUNDED: the full launch (per-query bounds); otherwise the sampled one.
-template <int KS, int METRIC, bool BOUNDED>
+template <int KS, int METRIC, bool BOUNDED, bool COLLECT = false>
 __global__ __launch_bounds__(256) void int8_gemm(Int8Planes pl, int64_t n,
                                                  const int8_t* __restrict__ qcodes,
                                                  const Int8QueryCoef* __restrict__ coefs, int64_t nq,
@@ -755,6 +762,10 @@ __global__ __launch_bounds__(256) void int8_gemm(Int8Planes pl, int64_t n,
     // Slots above `bound` never enter; keys above thr (the key of the
     // smaller of bound and the lane's largest slot) cannot pass.
     const uint64_t bound = !qvalid ? 0ull : (BOUNDED ? ga.qbound[qid] : kEmptySlot);
+    constexpr bool collect = BOUNDED && COLLECT;
+    uint64_t* cregion = collect ? ga.cbuf + (((size_t)(qvalid ? qid : 0) * ga.nseg + seg) * 2 + h) * ga.ccap
+                                : nullptr;
+    int ccnt = 0;
     float thr = !qvalid ? -__int_as_float(0x7F800000)
                         : (bound == kEmptySlot ? __int_as_float(0x7F800000) : slot_key(bound));
 
@@ -842,9 +853,14 @@ __global__ __launch_bounds__(256) void int8_gemm(Int8Planes pl, int64_t n,
                     const int m = 32 * (i >> 4) + 8 * ((i & 15) >> 2) + 4 * h + (i & 3);
                     const uint64_t slot = pack_slot(key[i], (uint32_t)(base + m));
                     if (slot <= bound) {
-                        lane_list_insert<C>(lst, slot);
-                        const uint64_t top = lst[C - 1] < bound ? lst[C - 1] : bound;
-                        thr = top == kEmptySlot ? thr : slot_key(top);
+                        if constexpr (collect) {
+                            if (ccnt < ga.ccap) cregion[ccnt] = slot;
+                            ++ccnt;
+                        } else {
+                            lane_list_insert<C>(lst, slot);
+                            const uint64_t top = lst[C - 1] < bound ? lst[C - 1] : bound;
+                            thr = top == kEmptySlot ? thr : slot_key(top);
+                        }
                     }
                 }
             }
@@ -887,7 +903,10 @@ __global__ __launch_bounds__(256) void int8_gemm(Int8Planes pl, int64_t n,
         prev1 = acc1;
     }
     offer(prev0, prev1, nst - 1, cb == 0 ? 2 : cb - 1);
-    if (qvalid) {
+    if (collect && qvalid) {
+        ga.ccount[((size_t)qid * ga.nseg + seg) * 2 + h] = ccnt < ga.ccap ? ccnt : ga.ccap;
+        if (ccnt > ga.ccap) atomicOr(&ga.cflag[qid], 1u);
+    } else if (qvalid) {
         uint64_t* out = ga.lists + (((size_t)qid * ga.nseg + seg) * 2 + h) * C;
 #pragma unroll
         for (int i = 0; i < C; ++i) out[i] = lst[i];
@@ -949,6 +968,185 @@ __global__ __launch_bounds__(256) void int8_lists_merge(
     __syncthreads();
     final_rescore_wide(queries + (int64_t)q * dim, coefs[q].qn, rows, norms, n, dim, metric, q, top,
                        ncand, kc, res, reinterpret_cast<float*>(cand), fa, proof, cut);
+}
+
+// Budget rounds over the slots the collect-mode contraction gathered
+// (grid (1, nq_launch), block 256; dynamic LDS: kI8CollectMergeLds bytes).
+// The query's regions are gathered into LDS; with `total` slots gathered at
+// or below the query's bound, the budget smallest slots of the corpus are
+// among them whenever budget <= total (BoundedExactScan.swift:96-121), so
+// each round selects them (radix select), rescores the rows it adds in the
+// dots.c order (16 lanes per row), takes the k smallest exact slots and
+// checks the proof.  Status as int8_collect: bits 0-1 the outcome (0 done,
+// 1 the next budget exceeds `total`, kStatusReselect: no round could run),
+// bits 2-7 the rounds run.
+constexpr int kI8GatherSlots = 8192;
+constexpr size_t kI8CollectMergeLds =
+    sizeof(uint64_t) * (256 + (size_t)kI8GatherSlots) + 2 * sizeof(uint32_t) * (size_t)kI8GatherSlots;
+
+template <int NCH>
+__global__ __launch_bounds__(256) void int8_collect_merge(
+    const float* __restrict__ rows, const float* __restrict__ norms, int64_t n, int dim,
+    const float* __restrict__ queries, const Int8QueryCoef* __restrict__ coefs, int metric, int kc,
+    int nreg, const uint64_t* __restrict__ cbuf, const int32_t* __restrict__ ccount,
+    const uint32_t* __restrict__ cflag, int ccap, int proof, FlatArgs fa) {
+    extern __shared__ uint64_t lds[];
+    uint64_t* top = lds;         // 256 slots: the k best exact slots
+    uint64_t* cand = lds + 256;  // kI8GatherSlots gathered key slots
+    float* exd = reinterpret_cast<float*>(cand + kI8GatherSlots);  // exact distances
+    uint32_t* fresh_pos = reinterpret_cast<uint32_t*>(exd + kI8GatherSlots);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lr = lane & 15, grp = wave * 4 + (lane >> 4), dim4 = dim >> 2;
+    const uint32_t q = blockIdx.y;
+    __shared__ int s_total, ntop;
+    __shared__ uint32_t hist[256];
+    if (cflag[q] != 0) {  // a region overflowed: select again with the lists
+        if (tid == 0) fa.status[q] = kStatusReselect;
+        return;
+    }
+    if (tid == 0) s_total = 0;
+    __syncthreads();
+    for (int r = tid; r < nreg; r += blockDim.x) {
+        const int c = ccount[(size_t)q * nreg + r];
+        if (c == 0) continue;
+        const int base = atomicAdd(&s_total, c);
+        const uint64_t* src = cbuf + ((size_t)q * nreg + r) * ccap;
+        for (int i = 0; i < c; ++i)
+            if (base + i < kI8GatherSlots) cand[base + i] = src[i];
+    }
+    __syncthreads();
+    const int64_t total = s_total;
+    if (total > kI8GatherSlots) {
+        if (tid == 0) fa.status[q] = kStatusReselect;
+        return;
+    }
+    __shared__ int s_nfresh;
+    const float* qp = queries + (int64_t)q * dim;
+    f4v qv[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const int idx = lr + 16 * c;
+        qv[c] = idx < dim4 ? *reinterpret_cast<const f4v*>(qp + 4 * idx) : f4v{0.f, 0.f, 0.f, 0.f};
+    }
+    const float qn = coefs[q].qn;
+    auto get = [&](int64_t i) { return cand[i]; };
+    uint64_t done_cut = 0;  // rows with slots at or below it are rescored (round > 1)
+    int64_t budget = kc;
+    for (int round = 1;; ++round) {
+        if (budget > total && total < n) {
+            if (tid == 0) fa.status[q] = round == 1 ? kStatusReselect : (uint8_t)(1 | ((round - 1) << 2));
+            return;
+        }
+        const int64_t nsel = budget < total ? budget : total;
+        uint64_t kth;
+        const uint64_t cut = block_radix_cut(get, total, (int)nsel, hist, &kth);
+        if (cut == kEmptySlot) {
+            uint64_t mx = 0;
+            for (int64_t i = tid; i < total; i += blockDim.x) mx = cand[i] > mx ? cand[i] : mx;
+            kth = block_reduce_u64<true>(mx);
+        }
+        // The positions this round adds, compacted; then their rows are
+        // rescored 16 at a time (one per 16-lane group), the next group's
+        // rows in flight.
+        if (tid == 0) s_nfresh = 0;
+        __syncthreads();
+        for (int64_t i0 = 0; i0 < total; i0 += blockDim.x) {
+            const int64_t i = i0 + tid;
+            const uint64_t sl = i < total ? cand[i] : kEmptySlot;
+            const bool fresh = i < total && sl <= cut && (round == 1 || sl > done_cut);
+            const uint64_t m = __ballot(fresh);
+            if (m == 0) continue;
+            int base = 0;
+            if (lane == 0) base = atomicAdd(&s_nfresh, __popcll(m));
+            base = __shfl(base, 0);
+            if (fresh) fresh_pos[base + __popcll(m & lanemask_lt())] = (uint32_t)i;
+        }
+        __syncthreads();
+        const int nfresh = s_nfresh;
+        auto load_row = [&](int j, f4v (&a)[NCH]) {
+            const bool v = j < nfresh;
+            const uint32_t pos = v ? fresh_pos[j] : 0u;
+            const uint32_t id = v ? slot_id(cand[pos]) : 0u;
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+                const int idx = lr + 16 * c;
+                a[c] = (v && idx < dim4) ? *reinterpret_cast<const f4v*>(rows + (int64_t)id * dim + 4 * idx)
+                                         : f4v{0.f, 0.f, 0.f, 0.f};
+            }
+        };
+        auto rescore = [&](int j, const f4v (&a)[NCH]) {
+            if (j >= nfresh) return;  // the whole group agrees
+            const uint32_t pos = fresh_pos[j];
+            const uint32_t id = slot_id(cand[pos]);
+            const float dot = chain_dot<NCH>(a, qv, dim4);
+            if (lr == 0) exd[pos] = host_distance(dot, qn, metric == kMetricIP ? 0.0f : norms[id], metric);
+        };
+        f4v ra[NCH], rb[NCH];
+        load_row(grp, ra);
+        for (int j0 = 0; j0 < nfresh; j0 += 32) {
+            load_row(j0 + 16 + grp, rb);
+            rescore(j0 + grp, ra);
+            load_row(j0 + 32 + grp, ra);
+            rescore(j0 + 16 + grp, rb);
+        }
+        done_cut = cut;
+        __syncthreads();  // exd[] is written
+        // The k smallest exact slots of the selection, sorted.
+        const int kout = (int64_t)fa.k < nsel ? fa.k : (int)nsel;
+        auto gete = [&](int64_t i) {
+            return cand[i] <= cut ? pack_slot(exd[i], slot_id(cand[i])) : kEmptySlot;
+        };
+        uint64_t ekth;
+        const uint64_t ecut = block_radix_cut(gete, total, kout, hist, &ekth);
+        if (tid == 0) ntop = 0;
+        __syncthreads();
+        for (int64_t i = tid; i < total; i += blockDim.x) {
+            if (cand[i] > cut) continue;
+            const uint64_t e = pack_slot(exd[i], slot_id(cand[i]));
+            if (e <= ecut) {
+                const int p = atomicAdd(&ntop, 1);
+                if (p < 256) top[p] = e;
+            }
+        }
+        __syncthreads();
+        const int nout = ntop < kout ? ntop : kout;
+        int sort_n = 64;
+        while (sort_n < nout) sort_n <<= 1;
+        for (int i = nout + tid; i < sort_n; i += blockDim.x) top[i] = kEmptySlot;
+        __syncthreads();
+        if (tid < 64) wave_bitonic_sort(top, sort_n);
+        __syncthreads();
+        const float cutoff = slot_key(kth);
+        const float tau = nout > 0 ? slot_key(top[nout - 1]) : 0.0f;
+        const bool all_rows = nsel >= n;
+        bool ok;
+        if (proof == kProofNone) {
+            ok = true;
+        } else if (proof == kProofMargin) {
+            // BoundedExactScan.swift:101-113
+            double margin = fabs((double)tau) * 1e-6;
+            margin = margin < 1e-7 ? 1e-7 : margin;
+            ok = all_rows || nsel < fa.k || (double)cutoff >= (double)tau + margin;
+        } else {
+            ok = all_rows || (nout > 0 && cutoff >= tau);
+        }
+        if (ok) {
+            for (int i = tid; i < fa.k_stride; i += blockDim.x) {
+                float dv = kFltMax;
+                uint32_t id = kEmptyId;
+                if (i < nout) {
+                    id = slot_id(top[i]);
+                    dv = slot_key(top[i]);
+                }
+                fa.out_dist[(int64_t)q * fa.k_stride + i] = dv;
+                fa.out_ids[(int64_t)q * fa.k_stride + i] = id;
+            }
+            if (tid == 0) fa.status[q] = (uint8_t)(round << 2);
+            return;
+        }
+        budget = budget * 4 < n ? budget * 4 : n;
+        __syncthreads();  // top[] and ntop are rewritten by the next round
+    }
 }
 
 // grid (1, nq): each query's bound, the kc-th smallest slot of its lists
@@ -1023,17 +1221,21 @@ static void launch_i8gemm_ks(const I8GemmPlan& p, const Int8Planes& pl, int64_t 
     const dim3 grid((unsigned)(ga.nseg * p.nqb));
     const size_t shmem = i8gemm_lds_bytes<KS>();
     const bool b = ga.qbound != nullptr;
+    const bool c = b && ga.ccap > 0;
     switch (metric) {
     case kMetricCosine:
-        if (b) hipLaunchKernelGGL((int8_gemm<KS, kMetricCosine, true>), grid, dim3(256), shmem, s, pl, n, qcodes, coefs, nq, ga);
+        if (c) hipLaunchKernelGGL((int8_gemm<KS, kMetricCosine, true, true>), grid, dim3(256), shmem, s, pl, n, qcodes, coefs, nq, ga);
+        else if (b) hipLaunchKernelGGL((int8_gemm<KS, kMetricCosine, true>), grid, dim3(256), shmem, s, pl, n, qcodes, coefs, nq, ga);
         else hipLaunchKernelGGL((int8_gemm<KS, kMetricCosine, false>), grid, dim3(256), shmem, s, pl, n, qcodes, coefs, nq, ga);
         break;
     case kMetricL2:
-        if (b) hipLaunchKernelGGL((int8_gemm<KS, kMetricL2, true>), grid, dim3(256), shmem, s, pl, n, qcodes, coefs, nq, ga);
+        if (c) hipLaunchKernelGGL((int8_gemm<KS, kMetricL2, true, true>), grid, dim3(256), shmem, s, pl, n, qcodes, coefs, nq, ga);
+        else if (b) hipLaunchKernelGGL((int8_gemm<KS, kMetricL2, true>), grid, dim3(256), shmem, s, pl, n, qcodes, coefs, nq, ga);
         else hipLaunchKernelGGL((int8_gemm<KS, kMetricL2, false>), grid, dim3(256), shmem, s, pl, n, qcodes, coefs, nq, ga);
         break;
     default:
-        if (b) hipLaunchKernelGGL((int8_gemm<KS, kMetricIP, true>), grid, dim3(256), shmem, s, pl, n, qcodes, coefs, nq, ga);
+        if (c) hipLaunchKernelGGL((int8_gemm<KS, kMetricIP, true, true>), grid, dim3(256), shmem, s, pl, n, qcodes, coefs, nq, ga);
+        else if (b) hipLaunchKernelGGL((int8_gemm<KS, kMetricIP, true>), grid, dim3(256), shmem, s, pl, n, qcodes, coefs, nq, ga);
         else hipLaunchKernelGGL((int8_gemm<KS, kMetricIP, false>), grid, dim3(256), shmem, s, pl, n, qcodes, coefs, nq, ga);
         break;
     }
@@ -1042,8 +1244,14 @@ static void launch_i8gemm_ks(const I8GemmPlan& p, const Int8Planes& pl, int64_t 
 static hipError_t launch_i8gemm(const I8GemmPlan& p, const Int8Planes& pl, int64_t n,
                                 const int8_t* qcodes, const Int8QueryCoef* coefs, int64_t nq,
                                 int metric, bool sampled, const uint64_t* qbound,
-                                uint64_t* lists, hipStream_t s) {
+                                uint64_t* lists, hipStream_t s, uint64_t* cbuf = nullptr,
+                                int32_t* ccount = nullptr, uint32_t* cflag = nullptr,
+                                int ccap = 0) {
     I8GemmArgs ga;
+    ga.cbuf = cbuf;
+    ga.ccount = ccount;
+    ga.cflag = cflag;
+    ga.ccap = ccap;
     ga.nseg = sampled ? p.s_nseg : p.nseg;
     ga.nqb = p.nqb;
     ga.rows_per_seg = sampled ? p.s_rows_per_seg : p.rows_per_seg;
@@ -1059,6 +1267,29 @@ static hipError_t launch_i8gemm(const I8GemmPlan& p, const Int8Planes& pl, int64
     case 12: launch_i8gemm_ks<12>(p, pl, n, qcodes, coefs, nq, metric, ga, s); break;
     default: return hipErrorInvalidValue;
     }
+    return hipGetLastError();
+}
+
+constexpr int kI8CollectCap = 128;       // slots per lane region of the collect launch
+constexpr int kI8CollectBoundKc = 256;   // the collect launch's bound: this many sampled slots
+
+template <int NCH>
+static hipError_t launch_i8_collect_merge(const float* rows, const float* norms, int64_t n,
+                                          int dim, const float* queries,
+                                          const Int8QueryCoef* coefs, int64_t nq, int metric,
+                                          int kc, int nreg, const uint64_t* cbuf,
+                                          const int32_t* ccount, const uint32_t* cflag, int proof,
+                                          const FlatArgs& fa, hipStream_t s) {
+    const size_t shmem = kI8CollectMergeLds;
+    static const bool attr = [shmem] {
+        (void)hipFuncSetAttribute((const void*)int8_collect_merge<NCH>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
+        return true;
+    }();
+    (void)attr;
+    hipLaunchKernelGGL(int8_collect_merge<NCH>, dim3(1, (unsigned)nq), dim3(256), shmem, s, rows,
+                       norms, n, dim, queries, coefs, metric, kc, nreg, cbuf, ccount, cflag,
+                       kI8CollectCap, proof, fa);
     return hipGetLastError();
 }
 
@@ -1172,6 +1403,16 @@ static bool int8_sampled_bounds() {
 static bool int8_collect_enabled() {
     static const bool on = [] {
         const char* e = std::getenv("MANS_INT8_COLLECT");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+
+// Mode-0 batches gather in the MFMA round and run the later budgets on what
+// it gathered (MANS_INT8_BATCH_COLLECT=0 keeps the lists).
+static bool int8_batch_collect_enabled() {
+    static const bool on = [] {
+        const char* e = std::getenv("MANS_INT8_BATCH_COLLECT");
         return !(e && e[0] == '0');
     }();
     return on;
@@ -1450,6 +1691,92 @@ static int int8_search_run(mans_ctx* ctx, mans_corpus* c, const float* d_q, int6
         return MANS_OK;
     };
 
+    // Mode-0 batches: the first round's contraction gathers every slot at or
+    // below a bound of max(kc, kI8CollectBoundKc) sampled slots, and one block
+    // per query runs the budget rounds on what was gathered
+    // (int8_collect_merge); queries it cannot serve repeat the round on the
+    // streaming scan.
+    auto gemm_collect_round = [&](const I8GemmPlan& gp, int64_t kc,
+                                  std::vector<std::pair<uint32_t, int64_t>>& next) -> int {
+        const int nreg = 2 * gp.nseg;
+        const size_t lbytes = (size_t)nq * gp.nseg * 2 * kI8List * sizeof(uint64_t);
+        const size_t cbytes = (size_t)nq * nreg * kI8CollectCap * sizeof(uint64_t);
+        const size_t nbytes = ((size_t)nq * nreg * sizeof(int32_t) + 255) / 256 * 256;
+        const size_t fbytes = ((size_t)nq * sizeof(uint32_t) + 255) / 256 * 256;
+        hipError_t e = slot->cand.ensure(lbytes + (size_t)nq * sizeof(uint64_t), ctx->fail_alloc);
+        if (e == hipSuccess) e = slot->aux2.ensure(cbytes + nbytes + fbytes, ctx->fail_alloc);
+        if (e == hipSuccess) e = slot->status_h.ensure((size_t)nq);
+        if (e != hipSuccess) return hip_fail(e, "int8 batch workspace");
+        uint64_t* lists = (uint64_t*)slot->cand.p;
+        uint64_t* qbound = lists + lbytes / sizeof(uint64_t);
+        uint64_t* cbuf = (uint64_t*)slot->aux2.p;
+        int32_t* ccount = (int32_t*)((char*)slot->aux2.p + cbytes);
+        uint32_t* cflag = (uint32_t*)((char*)slot->aux2.p + cbytes + nbytes);
+        const int64_t sampled_slots = (int64_t)2 * gp.s_nseg * kI8List;
+        const int bound_kc = (int)std::min<int64_t>(std::max<int64_t>(kc, kI8CollectBoundKc),
+                                                    sampled_slots / 2);
+        ctx->time_begin(slot, st);
+        e = hipMemsetAsync(cflag, 0, (size_t)nq * sizeof(uint32_t), st);
+        if (e == hipSuccess)
+            e = launch_i8gemm(gp, pl, n, qcodes, coefs, nq, (int)metric, true, nullptr, lists, st);
+        if (e == hipSuccess) {
+            hipLaunchKernelGGL(int8_lists_bound, dim3(1, (unsigned)nq), dim3(256),
+                               sampled_slots <= kKthLdsSlots ? sizeof(uint64_t) * (size_t)sampled_slots : 0,
+                               st, bound_kc, 2 * gp.s_nseg, (const uint64_t*)lists, qbound);
+            e = hipGetLastError();
+        }
+        ctx->time_end(slot, st, "int8_bound");
+        ctx->time_begin(slot, st);
+        if (e == hipSuccess)
+            e = launch_i8gemm(gp, pl, n, qcodes, coefs, nq, (int)metric, false, qbound, lists, st,
+                              cbuf, ccount, cflag, kI8CollectCap);
+        ctx->time_end(slot, st, "int8_gemm");
+        FlatArgs fa = {};
+        fa.out_dist = d_dist;
+        fa.out_ids = d_ids;
+        fa.status = (uint8_t*)slot->status_h.p;  // pinned: read after the stream syncs
+        fa.k = keff;
+        fa.k_stride = (int)k;
+        ctx->time_begin(slot, st);
+        if (e == hipSuccess) {
+            switch (nch) {
+            case 1: e = launch_i8_collect_merge<1>(rows, norms, n, dim, d_q, coefs, nq, (int)metric, (int)kc, nreg, cbuf, ccount, cflag, proof, fa, st); break;
+            case 2: e = launch_i8_collect_merge<2>(rows, norms, n, dim, d_q, coefs, nq, (int)metric, (int)kc, nreg, cbuf, ccount, cflag, proof, fa, st); break;
+            case 3: e = launch_i8_collect_merge<3>(rows, norms, n, dim, d_q, coefs, nq, (int)metric, (int)kc, nreg, cbuf, ccount, cflag, proof, fa, st); break;
+            case 4: e = launch_i8_collect_merge<4>(rows, norms, n, dim, d_q, coefs, nq, (int)metric, (int)kc, nreg, cbuf, ccount, cflag, proof, fa, st); break;
+            case 6: e = launch_i8_collect_merge<6>(rows, norms, n, dim, d_q, coefs, nq, (int)metric, (int)kc, nreg, cbuf, ccount, cflag, proof, fa, st); break;
+            case 8: e = launch_i8_collect_merge<8>(rows, norms, n, dim, d_q, coefs, nq, (int)metric, (int)kc, nreg, cbuf, ccount, cflag, proof, fa, st); break;
+            default: return fail(MANS_PIPELINE_UNAVAILABLE, "int8 scan: unsupported dim");
+            }
+        }
+        ctx->time_end(slot, st, "int8_merge");
+        if (e == hipSuccess) e = hipStreamSynchronize(st);
+        if (e != hipSuccess) return hip_fail(e, "int8 batch scan");
+        std::vector<uint32_t> redo;
+        const uint8_t* sh = (const uint8_t*)slot->status_h.p;
+        for (int64_t i = 0; i < nq; ++i) {
+            const int outcome = sh[i] & 3, ran = sh[i] >> 2;
+            if (outcome == kStatusReselect) {
+                redo.push_back((uint32_t)i);
+                continue;
+            }
+            rounds[i] += ran;
+            if (outcome == 1) {
+                int64_t b = kc;
+                for (int r = 0; r < ran; ++r) b = std::min<int64_t>(b * 4, n);
+                next.emplace_back((uint32_t)i, b);
+            }
+        }
+        ctx->reselects += (int64_t)redo.size();
+        if (!redo.empty()) {
+            std::vector<uint32_t> grow;
+            int rc = stream_round(redo, kc, true, grow);
+            if (rc != MANS_OK) return rc;
+            for (uint32_t qi : grow) next.emplace_back(qi, std::min<int64_t>(kc * 4, n));
+        }
+        return MANS_OK;
+    };
+
     // The first round of a batch on i8 MFMA; queries whose lists cannot
     // show an exact selection repeat the round on the streaming scan.
     auto gemm_round = [&](const I8GemmPlan& gp, int64_t kc, std::vector<uint32_t>& grow) -> int {
@@ -1558,6 +1885,8 @@ static int int8_search_run(mans_ctx* ctx, mans_corpus* c, const float* d_q, int6
         }
         if (collect) {
             rc = collect_round(cp, idx, bkc, next);
+        } else if (gemm && mode == 0 && int8_batch_collect_enabled()) {
+            rc = gemm_collect_round(gp, bkc, next);
         } else {
             std::vector<uint32_t> grow;
             rc = gemm ? gemm_round(gp, bkc, grow) : stream_round(idx, bkc, !first, grow);

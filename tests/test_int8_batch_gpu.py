@@ -85,9 +85,10 @@ def test_int8_batched_ragged(gpu_ctx):
 
 def test_int8_batched_crowded_segment_is_selected_again(gpu_ctx):
     # Every query's best rows sit in the first segment (near-copies of the
-    # queries in rows 0..399), more than its two 8-slot lane lists hold: the
-    # merge cannot show an exact selection, and the streaming scan selects
-    # those queries again at the same budget.
+    # queries in rows 0..399), more than its two 8-slot lane lists hold: in
+    # mode 1 the merge cannot show an exact selection, and the streaming
+    # scan selects those queries again at the same budget.  In mode 0 the
+    # contraction gathers into 128-slot regions, which hold them.
     dim, n, nq = 64, 40000, 20
     rng = np.random.default_rng(77)
     corpus = workloads.lcg_vectors(1, n, dim, seed=78)
@@ -100,7 +101,9 @@ def test_int8_batched_crowded_segment_is_selected_again(gpu_ctx):
     for metric, mode, budget in ((COS, 1, 100), (L2, 0, 0)):
         print(f"int8 crowded m{metric} mode{mode}", flush=True)
         gd, gi, rounds, launches = _batched(gpu_ctx, c, queries, 10, metric, mode, budget)
-        assert launches["int8_gemm"] == 1 and launches["int8_scan"] >= 1, launches
+        assert launches["int8_gemm"] == 1, launches
+        if mode == 1:
+            assert launches["int8_scan"] >= 1, launches
         ref = _oracle_rows(corpus, norms, planes, queries, 10, metric, mode=mode, budget=budget)
         _assert_same(gd, gi, ref, 10, f"crowded m{metric}")
         if mode == 1:
@@ -131,18 +134,18 @@ def test_int8_batched_mixture_1m_384(gpu_ctx):
     c.release()
 
 
-def test_int8_batched_mode0_pending_queries_collect(gpu_ctx):
-    # Mode 0 on the 1M x 384 mixture with 24 queries: the first round (budget
-    # 256) runs on i8 MFMA; the queries whose proof fails there (budget 1024
-    # on this mixture) go to one threshold-collect launch over just those
-    # queries, whose last blocks run the later budget rounds on the rows
-    # they gathered.  Results equal the exact flat search and the round
-    # counts equal the oracle's restatement of BoundedExactScan.
+def test_int8_batched_mode0_rounds_on_gathered_slots(gpu_ctx):
+    # Mode 0 on the 1M x 384 mixture with 24 queries: the MFMA contraction
+    # gathers every slot at or below a bound from 256 sampled slots, and one
+    # block per query runs the budget rounds (256, 1024, ...) on what was
+    # gathered; the mixture needs budget 1024 for most queries.  Results
+    # equal the exact flat search and the round counts equal the oracle's
+    # restatement of BoundedExactScan.
     print("int8 batched mode 0, 1M x 384 mixture, 24 queries", flush=True)
     db, q = workloads.mixture_1m_384(nq=24)
     c = gpu_ctx.upload(db)
     gd, gi, rounds, launches = _batched(gpu_ctx, c, q, 10, COS, 0, 0)
-    assert launches["int8_gemm"] == 1 and launches["int8_scan"] >= 1, launches
+    assert launches["int8_gemm"] == 1, launches
     fd, fi = c.flat_search(q, 10, COS)
     assert np.array_equal(gd, fd) and np.array_equal(gi, fi)
     assert np.any(rounds > 1)
@@ -152,4 +155,3 @@ def test_int8_batched_mode0_pending_queries_collect(gpu_ctx):
         final = oracle.int8_search(db, norms, planes, q[i], 10, COS)[2]
         assert rounds[i] == _rounds_for(final, 10, len(db)), f"query {i}"
     c.release()
-
