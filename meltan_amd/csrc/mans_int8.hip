@@ -971,7 +971,8 @@ __global__ __launch_bounds__(256) void int8_lists_merge(
 }
 
 // Budget rounds over the slots the collect-mode contraction gathered
-// (grid (1, nq_launch), block 256; dynamic LDS: kI8CollectMergeLds bytes).
+// (grid (1, nq_launch), block kI8MergeThreads; dynamic LDS:
+// kI8CollectMergeLds bytes).
 // The query's regions are gathered into LDS; with `total` slots gathered at
 // or below the query's bound, the budget smallest slots of the corpus are
 // among them whenever budget <= total (BoundedExactScan.swift:96-121), so
@@ -981,11 +982,12 @@ __global__ __launch_bounds__(256) void int8_lists_merge(
 // 1 the next budget exceeds `total`, kStatusReselect: no round could run),
 // bits 2-7 the rounds run.
 constexpr int kI8GatherSlots = 8192;
+constexpr int kI8MergeThreads = 512;  // one block per CU (the LDS): eight waves hide the row loads
 constexpr size_t kI8CollectMergeLds =
     sizeof(uint64_t) * (256 + (size_t)kI8GatherSlots) + 2 * sizeof(uint32_t) * (size_t)kI8GatherSlots;
 
 template <int NCH>
-__global__ __launch_bounds__(256) void int8_collect_merge(
+__global__ __launch_bounds__(kI8MergeThreads) void int8_collect_merge(
     const float* __restrict__ rows, const float* __restrict__ norms, int64_t n, int dim,
     const float* __restrict__ queries, const Int8QueryCoef* __restrict__ coefs, int metric, int kc,
     int nreg, const uint64_t* __restrict__ cbuf, const int32_t* __restrict__ ccount,
@@ -997,6 +999,7 @@ __global__ __launch_bounds__(256) void int8_collect_merge(
     uint32_t* fresh_pos = reinterpret_cast<uint32_t*>(exd + kI8GatherSlots);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lr = lane & 15, grp = wave * 4 + (lane >> 4), dim4 = dim >> 2;
+    constexpr int kGroups = kI8MergeThreads / 16;  // rows rescored per step
     const uint32_t q = blockIdx.y;
     __shared__ int s_total, ntop;
     __shared__ uint32_t hist[256];
@@ -1083,11 +1086,11 @@ __global__ __launch_bounds__(256) void int8_collect_merge(
         };
         f4v ra[NCH], rb[NCH];
         load_row(grp, ra);
-        for (int j0 = 0; j0 < nfresh; j0 += 32) {
-            load_row(j0 + 16 + grp, rb);
+        for (int j0 = 0; j0 < nfresh; j0 += 2 * kGroups) {
+            load_row(j0 + kGroups + grp, rb);
             rescore(j0 + grp, ra);
-            load_row(j0 + 32 + grp, ra);
-            rescore(j0 + 16 + grp, rb);
+            load_row(j0 + 2 * kGroups + grp, ra);
+            rescore(j0 + kGroups + grp, rb);
         }
         done_cut = cut;
         __syncthreads();  // exd[] is written
@@ -1287,7 +1290,7 @@ static hipError_t launch_i8_collect_merge(const float* rows, const float* norms,
         return true;
     }();
     (void)attr;
-    hipLaunchKernelGGL(int8_collect_merge<NCH>, dim3(1, (unsigned)nq), dim3(256), shmem, s, rows,
+    hipLaunchKernelGGL(int8_collect_merge<NCH>, dim3(1, (unsigned)nq), dim3(kI8MergeThreads), shmem, s, rows,
                        norms, n, dim, queries, coefs, metric, kc, nreg, cbuf, ccount, cflag,
                        kI8CollectCap, proof, fa);
     return hipGetLastError();
