@@ -433,11 +433,105 @@ static void launch_int8_scan(const FlatPlan& p, const Int8Planes& pl, const floa
 // 2-7 the rounds run.  A block with more than kCollectLdsSlots such rows, or
 // more than I8Collect::ccap of them in all, gives kStatusReselect and
 // nothing else is written (the caller selects again with the lists).
+// The budget rounds of BoundedExactScan.search (BoundedExactScan.swift:96-121)
+// over `total` gathered rows, run by one block: get(i) is the i-th gathered
+// key slot, gete(i, cut) its exact (distance, id) slot when its key slot is
+// at or below cut (else kEmptySlot).  With total rows gathered at or below
+// a bound, the budget smallest key slots of the corpus are among them
+// whenever budget <= total, so each round selects them (radix select),
+// takes the k smallest exact slots of the selection, sorts them and checks
+// the proof; a failed proof grows the budget 4x.  Writes the outputs of
+// query q and fa.status[y]: bits 0-1 the outcome (0 done, 1 the proof still
+// fails and the next budget exceeds total, kStatusReselect: no round could
+// run), bits 2-7 the rounds run.  top: 256 slots of LDS.
+template <class Get, class GetE>
+__device__ void i8_budget_rounds(Get&& get, GetE&& gete, int64_t total, int kc, int64_t n,
+                                 int proof, uint32_t q, uint32_t y, uint64_t* top, uint32_t* hist,
+                                 int* ntop, const FlatArgs& fa) {
+    const int tid = threadIdx.x;
+    int64_t budget = kc;
+    for (int round = 1;; ++round) {
+        if (budget > total && total < n) {
+            // The gathered rows no longer hold the budget smallest slots.
+            if (tid == 0) fa.status[y] = round == 1 ? kStatusReselect : (uint8_t)(1 | ((round - 1) << 2));
+            return;
+        }
+        // The selection: the budget smallest slots (every gathered row when
+        // they are all there is), and the largest of them.
+        const int64_t nsel = budget < total ? budget : total;
+        uint64_t kth;
+        const uint64_t cut = block_radix_cut(get, total, (int)nsel, hist, &kth);
+        if (cut == kEmptySlot) {
+            uint64_t mx = 0;
+            for (int64_t i = tid; i < total; i += blockDim.x) {
+                const uint64_t s = get(i);
+                mx = s > mx ? s : mx;
+            }
+            kth = block_reduce_u64<true>(mx);
+        }
+        // The k smallest exact slots of the selection, sorted.
+        const int kout = (int64_t)fa.k < nsel ? fa.k : (int)nsel;
+        uint64_t ekth;
+        const uint64_t ecut =
+            block_radix_cut([&](int64_t i) { return gete(i, cut); }, total, kout, hist, &ekth);
+        if (tid == 0) *ntop = 0;
+        __syncthreads();
+        for (int64_t i = tid; i < total; i += blockDim.x) {
+            const uint64_t e = gete(i, cut);
+            if (e != kEmptySlot && e <= ecut) {
+                const int p = atomicAdd(ntop, 1);
+                if (p < 256) top[p] = e;  // kout <= k <= 256 distinct slots
+            }
+        }
+        __syncthreads();
+        const int nout = *ntop < kout ? *ntop : kout;
+        int sort_n = 64;
+        while (sort_n < nout) sort_n <<= 1;
+        for (int i = nout + tid; i < sort_n; i += blockDim.x) top[i] = kEmptySlot;
+        __syncthreads();
+        if (tid < 64) wave_bitonic_sort(top, sort_n);
+        __syncthreads();
+        const float cutoff = slot_key(kth);
+        const float tau = nout > 0 ? slot_key(top[nout - 1]) : 0.0f;
+        const bool all_rows = nsel >= n;
+        bool ok;
+        if (proof == kProofNone) {
+            ok = true;
+        } else if (proof == kProofMargin) {
+            // BoundedExactScan.swift:101-113
+            double margin = fabs((double)tau) * 1e-6;
+            margin = margin < 1e-7 ? 1e-7 : margin;
+            ok = all_rows || nsel < fa.k || (double)cutoff >= (double)tau + margin;
+        } else {
+            ok = all_rows || (nout > 0 && cutoff >= tau);
+        }
+        if (ok) {
+            for (int i = tid; i < fa.k_stride; i += blockDim.x) {
+                float dv = kFltMax;
+                uint32_t id = kEmptyId;
+                if (i < nout) {
+                    id = slot_id(top[i]);
+                    dv = slot_key(top[i]);
+                }
+                fa.out_dist[(int64_t)q * fa.k_stride + i] = dv;
+                fa.out_ids[(int64_t)q * fa.k_stride + i] = id;
+            }
+            if (tid == 0) fa.status[y] = (uint8_t)(round << 2);
+            return;
+        }
+        budget = budget * 4 < n ? budget * 4 : n;
+        __syncthreads();  // top[] and *ntop are rewritten by the next round
+    }
+}
+
 struct I8Collect {
     const uint64_t* qbound;  // [nq]
     uint64_t* cbuf;          // [nq][ccap] slots (int8 keys)
     uint64_t* ebuf;          // [nq][ccap] exact (distance, id) slots
     int64_t ccap;
+    // Non-null: the last block only records the gathered count here and
+    // int8_collect_rounds runs the budget rounds.
+    int32_t* totals = nullptr;  // [nq]
 };
 constexpr int kCollectLdsSlots = 4096;  // rows gathered per block; candidates selected in LDS
 constexpr size_t kCollectShmem = sizeof(uint64_t) * (256 + kCollectLdsSlots);
@@ -536,7 +630,14 @@ __global__ __launch_bounds__(256) void int8_collect(
     __syncthreads();
     const int64_t total = s_total;
     if (total > cl.ccap) {
-        if (tid == 0) fa.status[y] = kStatusReselect;
+        if (tid == 0) {
+            fa.status[y] = kStatusReselect;
+            if (cl.totals) cl.totals[y] = -1;
+        }
+        return;
+    }
+    if (cl.totals) {  // a one-block launch runs the rounds from LDS
+        if (tid == 0) cl.totals[y] = (int32_t)total;
         return;
     }
     __shared__ uint32_t hist[256];
@@ -546,82 +647,50 @@ __global__ __launch_bounds__(256) void int8_collect(
         for (int64_t i = tid; i < total; i += blockDim.x) cand[i] = load_shared_slot(cbuf + i);
     __syncthreads();
     auto get = [&](int64_t i) { return in_lds ? cand[i] : load_shared_slot(cbuf + i); };
-    int64_t budget = kc;
-    for (int round = 1;; ++round) {
-        if (budget > total && total < n) {
-            // The gathered rows no longer hold the budget smallest slots.
-            if (tid == 0) fa.status[y] = round == 1 ? kStatusReselect : (uint8_t)(1 | ((round - 1) << 2));
-            return;
-        }
-        // The selection: the budget smallest slots (every gathered row when
-        // they are all there is), and the largest of them.
-        const int64_t nsel = budget < total ? budget : total;
-        uint64_t kth;
-        const uint64_t cut = block_radix_cut(get, total, (int)nsel, hist, &kth);
-        if (cut == kEmptySlot) {
-            uint64_t mx = 0;
-            for (int64_t i = tid; i < total; i += blockDim.x) {
-                const uint64_t s = get(i);
-                mx = s > mx ? s : mx;
-            }
-            kth = block_reduce_u64<true>(mx);
-        }
-        // The k smallest exact slots of the selection, sorted.
-        const int kout = (int64_t)fa.k < nsel ? fa.k : (int)nsel;
-        auto gete = [&](int64_t i) {
-            return get(i) <= cut ? load_shared_slot(ebuf + i) : kEmptySlot;
-        };
-        uint64_t ekth;
-        const uint64_t ecut = block_radix_cut(gete, total, kout, hist, &ekth);
-        if (tid == 0) ntop = 0;
-        __syncthreads();
-        for (int64_t i = tid; i < total; i += blockDim.x) {
-            if (get(i) > cut) continue;
-            const uint64_t e = load_shared_slot(ebuf + i);
-            if (e <= ecut) {
-                const int p = atomicAdd(&ntop, 1);
-                if (p < 256) top[p] = e;  // kout <= k <= 256 distinct slots
-            }
-        }
-        __syncthreads();
-        const int nout = ntop < kout ? ntop : kout;
-        int sort_n = 64;
-        while (sort_n < nout) sort_n <<= 1;
-        for (int i = nout + tid; i < sort_n; i += blockDim.x) top[i] = kEmptySlot;
-        __syncthreads();
-        if (tid < 64) wave_bitonic_sort(top, sort_n);
-        __syncthreads();
-        const float cutoff = slot_key(kth);
-        const float tau = nout > 0 ? slot_key(top[nout - 1]) : 0.0f;
-        const bool all_rows = nsel >= n;
-        bool ok;
-        if (proof == kProofNone) {
-            ok = true;
-        } else if (proof == kProofMargin) {
-            // BoundedExactScan.swift:101-113
-            double margin = fabs((double)tau) * 1e-6;
-            margin = margin < 1e-7 ? 1e-7 : margin;
-            ok = all_rows || nsel < fa.k || (double)cutoff >= (double)tau + margin;
-        } else {
-            ok = all_rows || (nout > 0 && cutoff >= tau);
-        }
-        if (ok) {
-            for (int i = tid; i < fa.k_stride; i += blockDim.x) {
-                float dv = kFltMax;
-                uint32_t id = kEmptyId;
-                if (i < nout) {
-                    id = slot_id(top[i]);
-                    dv = slot_key(top[i]);
-                }
-                fa.out_dist[(int64_t)q * fa.k_stride + i] = dv;
-                fa.out_ids[(int64_t)q * fa.k_stride + i] = id;
-            }
-            if (tid == 0) fa.status[y] = (uint8_t)(round << 2);
-            return;
-        }
-        budget = budget * 4 < n ? budget * 4 : n;
-        __syncthreads();  // top[] and ntop are rewritten by the next round
+    auto gete = [&](int64_t i, uint64_t cut) {
+        return get(i) <= cut ? load_shared_slot(ebuf + i) : kEmptySlot;
+    };
+    i8_budget_rounds(get, gete, total, kc, n, proof, q, y, top, hist, &ntop, fa);
+}
+
+// The budget rounds of the collect scan (grid (1, nq_launch), block
+// kI8RoundsThreads; dynamic LDS kI8RoundsLds): the row's gathered key
+// slots and exact slots are staged in LDS, then i8_budget_rounds; rows that
+// gathered more than kI8RoundsSlots run the rounds from global memory.
+constexpr int kI8RoundsSlots = 8192;
+constexpr int kI8RoundsThreads = 512;
+constexpr size_t kI8RoundsLds = sizeof(uint64_t) * (256 + 2 * (size_t)kI8RoundsSlots);
+
+__global__ __launch_bounds__(kI8RoundsThreads) void int8_collect_rounds(
+    int64_t n, const uint32_t* __restrict__ qidx, int kc, int proof, FlatArgs fa, I8Collect cl) {
+    extern __shared__ uint64_t lds[];
+    uint64_t* top = lds;
+    uint64_t* cand = lds + 256;
+    uint64_t* ex = cand + kI8RoundsSlots;
+    __shared__ uint32_t hist[256];
+    __shared__ int ntop;
+    const int tid = threadIdx.x;
+    const uint32_t y = blockIdx.y;
+    const uint32_t q = qidx ? qidx[y] : y;
+    const int32_t t = cl.totals[y];
+    if (t < 0) return;  // the collect launch already set the status
+    const int64_t total = t;
+    const uint64_t* cbuf = cl.cbuf + (int64_t)y * cl.ccap;
+    const uint64_t* ebuf = cl.ebuf + (int64_t)y * cl.ccap;
+    if (total > kI8RoundsSlots) {
+        auto getg = [&](int64_t i) { return cbuf[i]; };
+        auto geteg = [&](int64_t i, uint64_t cut) { return cbuf[i] <= cut ? ebuf[i] : kEmptySlot; };
+        i8_budget_rounds(getg, geteg, total, kc, n, proof, q, y, top, hist, &ntop, fa);
+        return;
     }
+    for (int64_t i = tid; i < total; i += blockDim.x) {
+        cand[i] = cbuf[i];
+        ex[i] = ebuf[i];
+    }
+    __syncthreads();
+    auto get = [&](int64_t i) { return cand[i]; };
+    auto gete = [&](int64_t i, uint64_t cut) { return cand[i] <= cut ? ex[i] : kEmptySlot; };
+    i8_budget_rounds(get, gete, total, kc, n, proof, q, y, top, hist, &ntop, fa);
 }
 
 template <int NCH>
@@ -1651,6 +1720,14 @@ static int int8_search_run(mans_ctx* ctx, mans_corpus* c, const float* d_q, int6
         cl.cbuf = fb.cand;
         cl.ebuf = fb.cand + (size_t)cnt * ccap;
         cl.ccap = ccap;
+        // Mode 0: the budget rounds run from LDS in a one-block launch per
+        // query after the collect launch (its last blocks only record their
+        // gathered counts).
+        const bool defer = proof == kProofMargin;
+        if (defer) {
+            if (e == hipSuccess) e = slot->aux2.ensure((size_t)cnt * sizeof(int32_t), ctx->fail_alloc);
+            cl.totals = (int32_t*)slot->aux2.p;
+        }
         ctx->time_begin(slot, st);
         if (e == hipSuccess) {
             switch (nch) {
@@ -1661,6 +1738,17 @@ static int int8_search_run(mans_ctx* ctx, mans_corpus* c, const float* d_q, int6
             case 6: e = launch_int8_collect<6>(p, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, (int)kc, proof, fa, cl, st); break;
             default: e = launch_int8_collect<8>(p, pl, rows, norms, n, dim, d_q, d_qidx, cnt, qcodes, coefs, (int)metric, (int)kc, proof, fa, cl, st); break;
             }
+        }
+        if (e == hipSuccess && defer) {
+            static const bool attr = [] {
+                (void)hipFuncSetAttribute((const void*)int8_collect_rounds,
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)kI8RoundsLds);
+                return true;
+            }();
+            (void)attr;
+            hipLaunchKernelGGL(int8_collect_rounds, dim3(1, (unsigned)cnt), dim3(kI8RoundsThreads),
+                               kI8RoundsLds, st, n, d_qidx, (int)kc, proof, fa, cl);
+            e = hipGetLastError();
         }
         ctx->time_end(slot, st, "int8_scan");
         if (e == hipSuccess) e = hipStreamSynchronize(st);
