@@ -158,30 +158,45 @@ __global__ __launch_bounds__(256) void ivf_plan(const uint32_t* __restrict__ pro
     }
 }
 
+// Exclusive scan of one value per thread of a 1024-thread block (wave
+// shuffles, then the 16 wave sums from LDS); *total gets the block's sum.
+template <typename T>
+__device__ __forceinline__ T block1024_exclusive_scan(T v, T* wsum, T* total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    T incl = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const T t = __shfl_up(incl, o);
+        if (lane >= o) incl += t;
+    }
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    T before = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) {
+        const T x = wsum[w];
+        before += w < wave ? x : (T)0;
+        all += x;
+    }
+    *total = all;
+    return before + incl - v;
+}
+
 // One block: exclusive scan of the per-query item counts, then the item ->
 // query map.  item_off[nq] holds the number of items.
 __global__ __launch_bounds__(1024) void ivf_items(const int32_t* __restrict__ nitems, int64_t nq,
                                                    int32_t* __restrict__ item_off,
                                                    int32_t* __restrict__ item_q) {
-    __shared__ int32_t part[1024];
+    __shared__ int32_t wsum[16];
     const int tid = threadIdx.x;
     const int64_t per = (nq + 1023) / 1024;
-    const int64_t a = tid * per, b = a + per < nq ? a + per : nq;
+    const int64_t a = tid * per < nq ? tid * per : nq;
+    const int64_t b = a + per < nq ? a + per : nq;
     int32_t s = 0;
     for (int64_t i = a; i < b; ++i) s += nitems[i];
-    part[tid] = s;
-    __syncthreads();
-    if (tid == 0) {
-        int32_t run = 0;
-        for (int t = 0; t < 1024; ++t) {
-            const int32_t v = part[t];
-            part[t] = run;
-            run += v;
-        }
-        item_off[nq] = run;
-    }
-    __syncthreads();
-    int32_t run = part[tid];
+    int32_t total;
+    int32_t run = block1024_exclusive_scan(s, wsum, &total);
+    if (tid == 0) item_off[nq] = total;
     for (int64_t i = a; i < b; ++i) {
         item_off[i] = run;
         for (int32_t j = 0; j < nitems[i]; ++j) item_q[run + j] = (int32_t)i;
@@ -453,7 +468,10 @@ struct LmShape {
     static constexpr size_t kTileOff = kQnOff + sizeof(float) * kLmQueries;
     static constexpr size_t kVnOff = kTileOff + sizeof(float) * kT * kRowF;
     static constexpr size_t kKeyOff = kVnOff + sizeof(float) * kT;
-    static constexpr int kKeyStride = kT + 1;             // keys per query, padded (banks)
+    // Keys per query, padded for the banks: the MFMA path writes rows 16 w + j
+    // of queries 4 g + r from lane 16 g + j (4 stride = 16 mod 64 banks), the
+    // VALU path query t % GP of row t / GP + ... from thread t.
+    static constexpr int kKeyStride = NCH <= 2 ? kT + 4 : kT + 1;
     static constexpr size_t kSelOff =
         (kKeyOff + sizeof(float) * kLmQueries * kKeyStride + 15) / 16 * 16;
     static constexpr size_t kBytes = kSelOff + sizeof(uint64_t) * kLmQueries * 128;
@@ -481,17 +499,17 @@ __global__ __launch_bounds__(256) void ivf_lm_count(const uint32_t* __restrict__
     if (i < pairs) atomicAdd(&lcount[probes[i]], 1);
 }
 
-// One block: lstart = exclusive scan of the pair counts, item_off = the
-// exclusive scan of each list's items (chunks x query groups); the counts
-// are zeroed for the fill.
+// One block: lstart = exclusive scan of the lists' pair counts, item_off
+// the same over their work items; lcount is cleared for ivf_lm_fill.
 __global__ __launch_bounds__(1024) void ivf_lm_lists(int32_t* __restrict__ lcount,
                                                      const int64_t* __restrict__ offsets, int nlist,
                                                      int32_t* __restrict__ lstart,
                                                      int32_t* __restrict__ item_off) {
-    __shared__ int32_t part_p[1024], part_i[1024];
+    __shared__ int32_t wsum_p[16], wsum_i[16];
     const int tid = threadIdx.x;
     const int per = (nlist + 1023) / 1024;
-    const int a = tid * per, b = a + per < nlist ? a + per : nlist;
+    const int a = tid * per < nlist ? tid * per : nlist;
+    const int b = a + per < nlist ? a + per : nlist;
     auto items_of = [&](int L, int32_t m) {
         const int64_t rows = offsets[L + 1] - offsets[L];
         if (m == 0 || rows == 0) return (int32_t)0;
@@ -502,23 +520,13 @@ __global__ __launch_bounds__(1024) void ivf_lm_lists(int32_t* __restrict__ lcoun
         sp += lcount[L];
         si += items_of(L, lcount[L]);
     }
-    part_p[tid] = sp;
-    part_i[tid] = si;
-    __syncthreads();
+    int32_t tp, ti;
+    int32_t rp = block1024_exclusive_scan(sp, wsum_p, &tp);
+    int32_t ri = block1024_exclusive_scan(si, wsum_i, &ti);
     if (tid == 0) {
-        int32_t rp = 0, ri = 0;
-        for (int t = 0; t < 1024; ++t) {
-            const int32_t vp = part_p[t], vi = part_i[t];
-            part_p[t] = rp;
-            part_i[t] = ri;
-            rp += vp;
-            ri += vi;
-        }
-        lstart[nlist] = rp;
-        item_off[nlist] = ri;
+        lstart[nlist] = tp;
+        item_off[nlist] = ti;
     }
-    __syncthreads();
-    int32_t rp = part_p[tid], ri = part_i[tid];
     for (int L = a; L < b; ++L) {
         const int32_t m = lcount[L];
         lstart[L] = rp;
@@ -529,18 +537,18 @@ __global__ __launch_bounds__(1024) void ivf_lm_lists(int32_t* __restrict__ lcoun
     }
 }
 
-// Thread per list: the descriptors of its work items (chunk-major within a
+// Wave per list: the descriptors of its work items (chunk-major within a
 // query group: item g nchunk + c).
 __global__ __launch_bounds__(256) void ivf_lm_items(const int32_t* __restrict__ item_off,
                                                     const int64_t* __restrict__ offsets, int nlist,
                                                     int2* __restrict__ items) {
-    const int L = blockIdx.x * 256 + threadIdx.x;
+    const int L = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (L >= nlist) return;
     const int first = item_off[L], count = item_off[L + 1] - first;
     if (count == 0) return;
     const int64_t rows = offsets[L + 1] - offsets[L];
     const int nchunk = (int)((rows + kLmRows - 1) / kLmRows);
-    for (int li = 0; li < count; ++li) {
+    for (int li = lane; li < count; li += 64) {
         const int g = li / nchunk, c = li - g * nchunk;
         items[first + li] = make_int2(L, c | (g << 16));
     }
@@ -599,25 +607,16 @@ __global__ __launch_bounds__(256) void ivf_lm_qplan(const uint32_t* __restrict__
 // One block: qbase = exclusive scan of the queries' list counts.
 __global__ __launch_bounds__(1024) void ivf_lm_qscan(const int32_t* __restrict__ qcount, int64_t nq,
                                                      int64_t* __restrict__ qbase) {
-    __shared__ int64_t part[1024];
+    __shared__ int64_t wsum[16];
     const int tid = threadIdx.x;
     const int64_t per = (nq + 1023) / 1024;
-    const int64_t a = tid * per, b = a + per < nq ? a + per : nq;
+    const int64_t a = tid * per < nq ? tid * per : nq;
+    const int64_t b = a + per < nq ? a + per : nq;
     int64_t sum = 0;
     for (int64_t i = a; i < b; ++i) sum += qcount[i];
-    part[tid] = sum;
-    __syncthreads();
-    if (tid == 0) {
-        int64_t run = 0;
-        for (int t = 0; t < 1024; ++t) {
-            const int64_t v = part[t];
-            part[t] = run;
-            run += v;
-        }
-        qbase[nq] = run;
-    }
-    __syncthreads();
-    int64_t run = part[tid];
+    int64_t total;
+    int64_t run = block1024_exclusive_scan(sum, wsum, &total);
+    if (tid == 0) qbase[nq] = total;
     for (int64_t i = a; i < b; ++i) {
         qbase[i] = run;
         run += qcount[i];
@@ -1008,7 +1007,7 @@ static int ivf_search_run(mans_ctx* ctx, const mans_ivf* ivf, const float* d_q, 
                                (int32_t*)la.item_off);
             hipLaunchKernelGGL(ivf_lm_fill, dim3(pblocks), dim3(256), 0, st, d_probes, pairs,
                                la.lstart, lcount, (int32_t*)la.lpairs);
-            hipLaunchKernelGGL(ivf_lm_items, dim3((unsigned)((nlist + 255) / 256)), dim3(256), 0, st,
+            hipLaunchKernelGGL(ivf_lm_items, dim3((unsigned)((nlist + 3) / 4)), dim3(256), 0, st,
                                la.item_off, (const int64_t*)ivf->offsets.p, nlist, (int2*)la.items);
             hipLaunchKernelGGL(ivf_lm_qplan, dim3((unsigned)((nq + 3) / 4)), dim3(256), 0, st,
                                d_probes, np, nq, (const int64_t*)ivf->offsets.p,
