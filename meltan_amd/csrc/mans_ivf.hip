@@ -692,7 +692,7 @@ __device__ __forceinline__ void lm_tile_keys_mfma(const float (&qa)[16 * NCH], c
     }
 }
 
-// Persistent grid over the work items; block 256; dynamic LDS
+// Grid of blocks striding over the work items; block 256; dynamic LDS
 // LmShape<NCH>::kBytes.  cand: kc slots per (query, chunk) list.
 template <int NCH>
 __global__ __launch_bounds__(256) void ivf_lm_scan(LmArgs la, int dim,
@@ -862,7 +862,17 @@ static hipError_t launch_lm(const LmArgs& la, const int64_t* qtotal, int64_t nq,
     // Products and partial sums the MFMA flushes below 2^-126 lose at most
     // 2^-126 each: 2 dim such terms in a dot, counted twice for L2's -2 dot.
     const float abs_slack = (float)(4.0 * dim * 1.1754943508222875e-38);
-    hipLaunchKernelGGL(ivf_lm_scan<NCH>, dim3(1024), dim3(256), S::kBytes, st, la, dim, queries,
+    // Far more blocks than fit on the chip (512 at two per CU): the
+    // dispatcher hands the next item to whichever CU frees first, which
+    // balances items of 1 to 8 tiles and 1 to 16 queries (measured at 1M x
+    // 128, nprobe 4 / 32: 2.52M / 824k queries/s with 1024 blocks looping
+    // over the items, 2.78M / 887k with 16384).  Blocks past the last item
+    // leave at once; larger batches loop.
+    static const unsigned grid = [] {
+        const char* ev = std::getenv("MANS_IVF_LM_BLOCKS");
+        return ev ? (unsigned)std::max(1, std::atoi(ev)) : 16384u;
+    }();
+    hipLaunchKernelGGL(ivf_lm_scan<NCH>, dim3(grid), dim3(256), S::kBytes, st, la, dim, queries,
                        metric, bc, abs_slack, kc, cand);
     const int cap = flat_cap_for(kc);
     hipLaunchKernelGGL(ivf_lm_merge<NCH>, dim3((unsigned)nq), dim3(256),
