@@ -432,6 +432,40 @@ __global__ __launch_bounds__(256) void ivf_probe_select(const float* __restrict_
     }
 }
 
+constexpr int kProbeWaveMax = 64;  // np served by ivf_probe_select_waves
+
+// Block per query, np <= kProbeWaveMax: the same np smallest (key, index)
+// slots as ivf_probe_select, ascending.  Wave w offers keys w 64 + 256 i to
+// its own list (WaveTopKT keeps the np smallest slots, ties by index), then
+// wave 0 takes the other three lists.  A NaN key counts as +inf.  The radix
+// cut's first passes put nearly every key of a query in one or two bins of
+// the float's top bytes, where the LDS atomics serialise; these lists look
+// at each key once.
+__global__ __launch_bounds__(256) void ivf_probe_select_waves(const float* __restrict__ keys,
+                                                              int nlist, int np,
+                                                              uint32_t* __restrict__ probes) {
+    __shared__ uint64_t lists[4 * 128];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t q = blockIdx.x;
+    const float* kq = keys + q * nlist;
+    WaveTopKT<128> sel;
+    sel.init(lists + wave * 128, 128, np);
+    for (int base = wave * 64; base < nlist; base += 256) {
+        const int c = base + lane;
+        const bool v = c < nlist;
+        float key = v ? kq[c] : 0.0f;
+        key = key == key ? key : __int_as_float(0x7F800000);
+        sel.offer(v, key, (uint32_t)c);
+    }
+    sel.finish();
+    __syncthreads();
+    if (wave == 0) {
+        for (int w = 1; w < 4; ++w) sel.offer_slots(lists + w * 128, np);
+        sel.finish();
+        if (lane < np) probes[q * np + lane] = slot_id(lists[lane]);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // List-major batch scan (first round of a batch of at least kLmMinBatch
 // queries).  The per-query scan above reads a list once for every query
@@ -924,9 +958,15 @@ static int ivf_search_run(mans_ctx* ctx, const mans_ivf* ivf, const float* d_q, 
         hipLaunchKernelGGL(ivf_coarse_keys, grid, dim3(256), sizeof(float) * (kCoarseQ * dim + kCoarseQ),
                            st, d_q + q0 * dim, m, dim, (const float*)ivf->cent_t.p,
                            (const float*)ivf->cent->norms.p, nlist_i, (int)metric, (float*)slot->aux0.p);
-        hipLaunchKernelGGL(ivf_probe_select, dim3((unsigned)m), dim3(256),
-                           nlist_i <= kProbeLdsSlots ? sizeof(uint64_t) * nlist_i : 0, st,
-                           (const float*)slot->aux0.p, nlist_i, np, (uint32_t*)slot->aux1.p + q0 * np);
+        if (np <= kProbeWaveMax)
+            hipLaunchKernelGGL(ivf_probe_select_waves, dim3((unsigned)m), dim3(256), 0, st,
+                               (const float*)slot->aux0.p, nlist_i, np,
+                               (uint32_t*)slot->aux1.p + q0 * np);
+        else
+            hipLaunchKernelGGL(ivf_probe_select, dim3((unsigned)m), dim3(256),
+                               nlist_i <= kProbeLdsSlots ? sizeof(uint64_t) * nlist_i : 0, st,
+                               (const float*)slot->aux0.p, nlist_i, np,
+                               (uint32_t*)slot->aux1.p + q0 * np);
         e = hipGetLastError();
     }
     ctx->time_end(slot, st, "ivf_probe");

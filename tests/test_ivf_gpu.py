@@ -83,6 +83,29 @@ def test_ivf_list_major_batch_matches_oracle(gpu_ctx, dim):
         c.release()
 
 
+def test_ivf_probe_selection_both_paths_and_ties(gpu_ctx):
+    # nprobe <= 64 selects with per-wave lists, above it with the radix cut;
+    # every centroid appears twice (rows 0..149 repeated), so each query's
+    # keys come in equal pairs and the (distance, index) order decides.
+    dim, n = 64, 8000
+    rows = workloads.lcg_vectors(1, n, dim, seed=631)
+    base = rows[:150].copy()
+    cents = np.concatenate([base, base])
+    part = oracle.IVFPartition(rows, cents, L2)
+    c = gpu_ctx.upload(rows)
+    ivf = c.ivf_flat_build(cents, L2)
+    queries = workloads.lcg_vectors(1, 70, dim, seed=632)
+    for nprobe in (63, 64, 65, 200):
+        print(f"ivf probe selection nprobe{nprobe}", flush=True)
+        gd, gi, gp = ivf.search(queries, 10, nprobe, want_probes=True)
+        for qi in range(queries.shape[0]):
+            od, oi, op = part.search(queries[qi], 10, nprobe)
+            assert np.array_equal(gp[qi], op), f"probes np{nprobe} q{qi}"
+            _assert_rows(gd[qi], gi[qi], od, oi, f"np{nprobe} q{qi}")
+    ivf.release()
+    c.release()
+
+
 def test_ivf_full_probe_equals_flat(gpu_ctx):
     dim, n, nlist = 128, 5000, 20
     rows = workloads.lcg_vectors(0, n, dim, seed=611)
