@@ -367,24 +367,25 @@ __global__ __launch_bounds__(256) void ivf_transpose(const float* __restrict__ s
 
 constexpr int kCoarseQ = 16;  // queries per block row
 
-// grid (ceil(nlist / 256), ceil(nq / kCoarseQ)); block 256; dynamic LDS
-// (kCoarseQ dim + kCoarseQ) floats.  keys: [nq][nlist].
+// grid (ceil(nlist / 256), ceil(nq / kCoarseQ)); block 256; dim a multiple
+// of 4.  keys: [nq][nlist].  Thread per centroid, kCoarseQ queries per
+// block: the queries' elements are uniform across the block and come in
+// through scalar loads, so the loop is the centroid column load and the
+// mul + add of each (query, dim) in the dots.c order.
 __global__ __launch_bounds__(256) void ivf_coarse_keys(const float* __restrict__ queries, int64_t nq,
                                                        int dim, const float* __restrict__ cent_t,
                                                        const float* __restrict__ cnorms, int nlist,
                                                        int metric, float* __restrict__ keys) {
-    extern __shared__ float cq[];
-    float* cqn = cq + kCoarseQ * dim;
+    __shared__ float cqn[kCoarseQ];
     const int tid = threadIdx.x;
     const int64_t q0 = (int64_t)blockIdx.y * kCoarseQ;
-    for (int i = tid; i < kCoarseQ * dim; i += blockDim.x) {
-        const int j = i / dim;
-        cq[i] = q0 + j < nq ? queries[(q0 + j) * dim + (i - j * dim)] : 0.0f;
-    }
-    __syncthreads();
+    const float* qrow[kCoarseQ];
+#pragma unroll
+    for (int j = 0; j < kCoarseQ; ++j) qrow[j] = queries + (q0 + j < nq ? q0 + j : nq - 1) * dim;
     if (tid < kCoarseQ) {
+        const float* qp = queries + (q0 + tid < nq ? q0 + tid : nq - 1) * dim;
         float s = 0.0f;
-        for (int d = 0; d < dim; ++d) s = s + cq[tid * dim + d] * cq[tid * dim + d];
+        for (int d = 0; d < dim; ++d) s = s + qp[d] * qp[d];
         cqn[tid] = metric == kMetricIP ? 0.0f : s;
     }
     __syncthreads();
@@ -393,10 +394,18 @@ __global__ __launch_bounds__(256) void ivf_coarse_keys(const float* __restrict__
     float acc[kCoarseQ];
 #pragma unroll
     for (int j = 0; j < kCoarseQ; ++j) acc[j] = 0.0f;
-    for (int d = 0; d < dim; ++d) {
-        const float b = cent_t[(int64_t)d * nlist + c];
+    for (int d0 = 0; d0 < dim; d0 += 4) {
+        float b[4];
 #pragma unroll
-        for (int j = 0; j < kCoarseQ; ++j) acc[j] = acc[j] + cq[j * dim + d] * b;
+        for (int t = 0; t < 4; ++t) b[t] = cent_t[(int64_t)(d0 + t) * nlist + c];
+#pragma unroll
+        for (int j = 0; j < kCoarseQ; ++j) {
+            const f4v qv = *reinterpret_cast<const f4v*>(qrow[j] + d0);
+            acc[j] = acc[j] + qv.x * b[0];
+            acc[j] = acc[j] + qv.y * b[1];
+            acc[j] = acc[j] + qv.z * b[2];
+            acc[j] = acc[j] + qv.w * b[3];
+        }
     }
     const float cn = metric == kMetricIP ? 0.0f : cnorms[c];
 #pragma unroll
@@ -484,7 +493,10 @@ __global__ __launch_bounds__(256) void ivf_probe_select_waves(const float* __res
 // entry of the kc best has fewer than kc smaller keys in its own chunk), so
 // the per-query merge, exact rescore and proof are those of the per-query
 // scan; queries whose proof fails go back to it with a larger candidate
-// count.
+// count.  A chunk list that fills lowers its query's shared bound (the
+// smallest kc-th key of any filled list, an upper bound on the query's kc-th
+// key over all its rows); later items of the query offer only keys at or
+// below it.  The rows this turns away have keys above the merge's cutoff.
 constexpr int kLmRows = 512;
 constexpr int kLmQueries = 16;
 constexpr int64_t kLmMinBatch = 64;
@@ -522,6 +534,7 @@ struct LmArgs {
     const int2* items;        // [items] (list, chunk + group << 16) of each work item
     const int32_t* qchunk;    // [nq][np] the query's first chunk list of probe p
     const int64_t* qbase;     // [nq + 1] the query's first candidate list
+    uint32_t* qbound;         // [nq] ordered bits of a bound on the query's kc-th key
     int np;
     int nlist;
 };
@@ -599,13 +612,18 @@ __global__ __launch_bounds__(256) void ivf_lm_fill(const uint32_t* __restrict__ 
     lpairs[lstart[L] + atomicAdd(&lfill[L], 1)] = (int32_t)i;
 }
 
+// No bound on a query's kc-th key yet (above every ordered key).
+constexpr uint32_t kNoBound = 0xFFFFFFFFu;
+
 // Wave per query: the first chunk list of each probe among the query's
-// lists, the query's list count and its probed rows.
+// lists, the query's list count and its probed rows; its kc-th key bound is
+// reset.
 __global__ __launch_bounds__(256) void ivf_lm_qplan(const uint32_t* __restrict__ probes, int np,
                                                     int64_t nq, const int64_t* __restrict__ offsets,
                                                     int32_t* __restrict__ qchunk,
                                                     int32_t* __restrict__ qcount,
-                                                    int64_t* __restrict__ qtotal) {
+                                                    int64_t* __restrict__ qtotal,
+                                                    uint32_t* __restrict__ qbound) {
     const int lane = threadIdx.x & 63;
     const int64_t q = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (q >= nq) return;  // the whole wave leaves together
@@ -635,6 +653,7 @@ __global__ __launch_bounds__(256) void ivf_lm_qplan(const uint32_t* __restrict__
     if (lane == 0) {
         qcount[q] = carry;
         qtotal[q] = rows_all;
+        qbound[q] = kNoBound;
     }
 }
 
@@ -754,6 +773,15 @@ __global__ __launch_bounds__(256) void ivf_lm_scan(LmArgs la, int dim,
         const int gp = mg <= S::kMinGp ? S::kMinGp : (mg <= 8 ? 8 : 16);
         const int64_t a = r0 + (int64_t)c * kLmRows;
         const int64_t b = a + kLmRows < r0 + nrows ? a + kLmRows : r0 + nrows;
+        uint32_t qbound_in[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int qq = wave + 4 * i;
+            qbound_in[i] = kNoBound;
+            if (qq < mg)
+                qbound_in[i] = __hip_atomic_load(la.qbound + la.lpairs[p0 + qq] / la.np,
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
         __syncthreads();  // the previous item is done with the LDS
         for (int e = tid; e < kLmQueries * 16 * NCH; e += 256) {
             const int qq = e / (16 * NCH), d4 = e - qq * 16 * NCH;
@@ -795,7 +823,15 @@ __global__ __launch_bounds__(256) void ivf_lm_scan(LmArgs la, int dim,
         // Wave w keeps the selections of queries w, w + 4, w + 8, w + 12.
         WaveTopKT<128> sel[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sel[i].init(selbuf + (wave + 4 * i) * 128, 128, kc);
+        for (int i = 0; i < 4; ++i) {
+            sel[i].init(selbuf + (wave + 4 * i) * 128, 128, kc);
+            // A chunk list of the same query that has already filled gives
+            // a bound on the query's kc-th key: rows above it are not among
+            // the query's kc smallest keys, and every row this list turns
+            // away still has a key above the merge's cutoff.
+            const uint32_t qb = qbound_in[i];
+            if (qb != kNoBound) sel[i].thresh = from_ordered_bits(qb);
+        }
         // Row tiles, the next one's loads in flight during the current one's dots.
         f4v pf[S::kLoads];
         float pvn = 0.0f;
@@ -851,6 +887,8 @@ __global__ __launch_bounds__(256) void ivf_lm_scan(LmArgs la, int dim,
             uint64_t* dst = cand + (la.qbase[q] + la.qchunk[(int64_t)q * la.np + pr] + c) * (int64_t)kc;
             for (int sidx = lane; sidx < kc; sidx += 64)
                 dst[sidx] = sidx < sel[i].count ? sel[i].buf[sidx] : kEmptySlot;
+            if (sel[i].count == kc && lane == 0)
+                atomicMin(la.qbound + q, ordered_bits(slot_key(sel[i].buf[kc - 1])));
         }
     }
 }
@@ -955,8 +993,7 @@ static int ivf_search_run(mans_ctx* ctx, const mans_ivf* ivf, const float* d_q, 
     for (int64_t q0 = 0; q0 < nq && e == hipSuccess; q0 += pchunk) {
         const int64_t m = std::min<int64_t>(pchunk, nq - q0);
         const dim3 grid((unsigned)((nlist_i + 255) / 256), (unsigned)((m + kCoarseQ - 1) / kCoarseQ));
-        hipLaunchKernelGGL(ivf_coarse_keys, grid, dim3(256), sizeof(float) * (kCoarseQ * dim + kCoarseQ),
-                           st, d_q + q0 * dim, m, dim, (const float*)ivf->cent_t.p,
+        hipLaunchKernelGGL(ivf_coarse_keys, grid, dim3(256), 0, st, d_q + q0 * dim, m, dim, (const float*)ivf->cent_t.p,
                            (const float*)ivf->cent->norms.p, nlist_i, (int)metric, (float*)slot->aux0.p);
         if (np <= kProbeWaveMax)
             hipLaunchKernelGGL(ivf_probe_select_waves, dim3((unsigned)m), dim3(256), 0, st,
@@ -1023,6 +1060,7 @@ static int ivf_search_run(mans_ctx* ctx, const mans_ivf* ivf, const float* d_q, 
         const size_t o_item = take((size_t)(nlist + 1) * 4), o_pairs = take((size_t)pairs * 4);
         const size_t o_qchunk = take((size_t)pairs * 4), o_qcount = take((size_t)nq * 4);
         const size_t o_qbase = take((size_t)(nq + 1) * 8), o_qtotal = take((size_t)nq * 8);
+        const size_t o_qbound = take((size_t)nq * 4);
         // Work items: at most one per (query, chunk of a probed list) plus
         // one per (list, chunk) for the partial query groups.
         const int64_t items_bound = lists_bound + ivf->n / kLmRows + nlist;
@@ -1045,6 +1083,7 @@ static int ivf_search_run(mans_ctx* ctx, const mans_ivf* ivf, const float* d_q, 
         la.items = (const int2*)(base + o_items);
         la.qchunk = (const int32_t*)(base + o_qchunk);
         la.qbase = (const int64_t*)(base + o_qbase);
+        la.qbound = (uint32_t*)(base + o_qbound);
         la.np = np;
         la.nlist = nlist;
         const int64_t* qtotal = (const int64_t*)(base + o_qtotal);
@@ -1062,7 +1101,7 @@ static int ivf_search_run(mans_ctx* ctx, const mans_ivf* ivf, const float* d_q, 
             hipLaunchKernelGGL(ivf_lm_qplan, dim3((unsigned)((nq + 3) / 4)), dim3(256), 0, st,
                                d_probes, np, nq, (const int64_t*)ivf->offsets.p,
                                (int32_t*)la.qchunk, (int32_t*)(base + o_qcount),
-                               (int64_t*)qtotal);
+                               (int64_t*)qtotal, la.qbound);
             hipLaunchKernelGGL(ivf_lm_qscan, dim3(1), dim3(1024), 0, st,
                                (const int32_t*)(base + o_qcount), nq, (int64_t*)la.qbase);
             e = hipGetLastError();
