@@ -553,13 +553,23 @@ __device__ __forceinline__ int32_t lm_items_of(int64_t rows, int32_t m) {
     return (int32_t)(((rows + kLmRows - 1) / kLmRows) * ((m + kLmQueries - 1) / kLmQueries));
 }
 
+// Class of a list's work rows x m on a half-octave scale (0 .. 63).
+__device__ __forceinline__ int lm_work_class(int64_t rows, int32_t m) {
+    const uint64_t x = (uint64_t)rows * (uint64_t)m;
+    if (x < 2) return 0;
+    const int fl = 63 - __clzll((long long)x);
+    const int c = 2 * fl + (int)((x >> (fl - 1)) & 1);
+    return c < 63 ? c : 63;
+}
+
 // One block: lstart = exclusive scan of the lists' pair counts; item_off[L]
 // = the first work item of list L, with the lists laid out by ascending
-// item count (classes min(items, 63), any order within a class): the short
-// items run first and their filled chunk lists set their queries' shared
-// kc-th key bounds before the long items of the same queries start (at 1M
-// x 128, nprobe 4 / 32: scan 178 / 637 us in list order, 184 / 636 longest
-// first, 157 / 585 shortest first).  item_off[nlist] = the number of items.
+// work (rows x probing queries, half-octave classes, any order within a
+// class): the short items run first and their filled chunk lists set their
+// queries' shared kc-th key bounds before the long items of the same
+// queries start (at 1M x 128, nprobe 4 / 32: scan 178 / 637 us in list
+// order, 184 / 636 longest first by item count, 157 / 585 shortest first by
+// item count, 149 / 581 by work).  item_off[nlist] = the number of items.
 // The order of the items changes no result (each writes its own candidate
 // lists).  lcount is cleared for ivf_lm_fill.
 __global__ __launch_bounds__(1024) void ivf_lm_lists(int32_t* __restrict__ lcount,
@@ -582,8 +592,9 @@ __global__ __launch_bounds__(1024) void ivf_lm_lists(int32_t* __restrict__ lcoun
     int32_t tp;
     int32_t rp = block1024_exclusive_scan(sp, wsum_p, &tp);  // its barrier orders the clears
     for (int L = a; L < b; ++L) {
-        const int32_t ni = lm_items_of(offsets[L + 1] - offsets[L], lcount[L]);
-        if (ni > 0) atomicAdd(&class_items[ni < kClasses - 1 ? ni : kClasses - 1], ni);
+        const int64_t rows = offsets[L + 1] - offsets[L];
+        const int32_t ni = lm_items_of(rows, lcount[L]);
+        if (ni > 0) atomicAdd(&class_items[lm_work_class(rows, lcount[L])], ni);
     }
     __syncthreads();
     if (tid < 64) {
@@ -602,8 +613,9 @@ __global__ __launch_bounds__(1024) void ivf_lm_lists(int32_t* __restrict__ lcoun
     __syncthreads();
     for (int L = a; L < b; ++L) {
         const int32_t m = lcount[L];
-        const int32_t ni = lm_items_of(offsets[L + 1] - offsets[L], m);
-        const int cls = ni < kClasses - 1 ? ni : kClasses - 1;
+        const int64_t rows = offsets[L + 1] - offsets[L];
+        const int32_t ni = lm_items_of(rows, m);
+        const int cls = lm_work_class(rows, m);
         lstart[L] = rp;
         item_off[L] = ni > 0 ? class_base[cls] + atomicAdd(&class_fill[cls], ni) : 0;
         rp += m;
