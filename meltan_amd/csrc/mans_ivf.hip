@@ -777,12 +777,19 @@ __device__ __forceinline__ void lm_tile_keys_mfma(const float (&qa)[16 * NCH], c
     const int row = 16 * wave + j;
     if (row < nvalid) {
         const float v = vn[row];
+        auto put = [&](auto key_of) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int q = 4 * g + r;
-            tkeys[q * S::kKeyStride + row] =
-                lower_key(c0[r] + c1[r], qnorm[q], v, metric, bc) - abs_slack;
-        }
+            for (int r = 0; r < 4; ++r) {
+                const int q = 4 * g + r;
+                tkeys[q * S::kKeyStride + row] = key_of(c0[r] + c1[r], qnorm[q]) - abs_slack;
+            }
+        };
+        if (metric == kMetricL2)
+            put([&](float f, float qn) { return lower_key_m<kMetricL2>(f, qn, v, bc); });
+        else if (metric == kMetricIP)
+            put([&](float f, float qn) { return lower_key_m<kMetricIP>(f, qn, v, bc); });
+        else
+            put([&](float f, float qn) { return lower_key_m<kMetricCosine>(f, qn, v, bc); });
     }
 }
 

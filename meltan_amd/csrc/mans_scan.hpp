@@ -41,6 +41,27 @@ __device__ __forceinline__ float lower_key(float f, float qn, float vn, int metr
     return metric == kMetricIP ? k_ip : (metric == kMetricL2 ? k_l2 : k_cos);
 }
 
+// lower_key for one metric known at the call (the same expressions as its
+// branch there): for callers outside a load-pipelined loop, where a uniform
+// branch on the metric costs nothing and the other metrics' square root and
+// division are not evaluated.
+template <int METRIC>
+__device__ __forceinline__ float lower_key_m(float f, float qn, float vn, const BoundCoef& bc) {
+    const float s = sqrtf(qn * vn);
+    if constexpr (METRIC == kMetricIP) {
+        return -f - s * bc.c_ip;
+    } else if constexpr (METRIC == kMetricL2) {
+        float dd = qn - 2.0f * f + vn;
+        dd = dd > 0.0f ? dd : 0.0f;
+        return dd - (qn + vn + 2.0f * s) * bc.c_l2;
+    } else {
+        float k_cos = (1.0f - f / s) - bc.eps_cos;
+        k_cos = s < 1.001e-10f ? -1.0f : k_cos;
+        k_cos = vn == 0.0f ? 1.0f - bc.eps_cos : k_cos;
+        return k_cos;
+    }
+}
+
 // Loads of the streaming pass: R rows per 16-lane group (rows base + 4 wave
 // + grp + 16 j), clamped to the block's last row and, past the row's end,
 // replaced by zeros, so that no branch separates the loads.  The scheduling
