@@ -501,6 +501,7 @@ constexpr int kLmRows = 512;
 constexpr int kLmQueries = 16;
 constexpr int64_t kLmMinBatch = 64;
 constexpr int kLmMaxNch = 4;  // dim <= 256
+constexpr int kLmMergeCap = 128;  // merge selection slots per wave (kc <= 64)
 
 template <int NCH>
 struct LmShape {
@@ -961,7 +962,7 @@ __global__ __launch_bounds__(256) void ivf_lm_merge(LmArgs la, const int64_t* __
         qv[c] = idx < dim4 ? *reinterpret_cast<const f4v*>(qp + 4 * idx) : f4v{0.f, 0.f, 0.f, 0.f};
     }
     const int64_t first = la.qbase[q], nlists = la.qbase[q + 1] - first;
-    WaveTopK sel;
+    WaveTopKT<kLmMergeCap> sel;  // the sorts compiled for 128 slots
     block_select_lists(cand + first * kc, nlists * kc, lds, cap, kc, sel);
     final_rescore_f4<NCH>(qv, la.packed, la.packed_norms, qtotal[q], dim, metric, q, lds, kc, fa,
                           kFltMax, kProofFlat, list_ids, (int)q);
@@ -995,6 +996,7 @@ static hipError_t launch_lm(const LmArgs& la, const int64_t* qtotal, int64_t nq,
     hipLaunchKernelGGL(ivf_lm_scan<NCH>, dim3(grid), dim3(256), S::kBytes, st, la, dim, queries,
                        metric, bc, abs_slack, kc, cand);
     const int cap = flat_cap_for(kc);
+    if (cap != kLmMergeCap) return hipErrorInvalidValue;  // kc <= 64 on this path
     hipLaunchKernelGGL(ivf_lm_merge<NCH>, dim3((unsigned)nq), dim3(256),
                        sizeof(uint64_t) * 4 * (size_t)cap, st, la, qtotal, dim, queries, list_ids,
                        metric, kc, cap, (const uint64_t*)cand, fa);
