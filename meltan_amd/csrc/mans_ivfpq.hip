@@ -279,6 +279,9 @@ __global__ __launch_bounds__(256) void pq_coarse_dist(const float* __restrict__ 
 // When more centroids tie at the np-th distance than those kept (a zero
 // query, duplicate centroids), the list is replayed over every centroid in
 // index order instead.  dynamic LDS: 4 * cap slots; cap >= 2 np + 128.
+// CAP: the lists' capacity when fixed at compile time (the sorts compiled
+// for it; 256 for np <= 64), else 0.
+template <int CAP>
 __global__ __launch_bounds__(256) void pq_probes(const float* __restrict__ dists, int nlist,
                                                  int np, int kc, int cap,
                                                  uint32_t* __restrict__ probes) {
@@ -287,7 +290,7 @@ __global__ __launch_bounds__(256) void pq_probes(const float* __restrict__ dists
     const int tid = threadIdx.x, wave = tid >> 6;
     const int64_t q = blockIdx.x;
     const float* qd = dists + q * nlist;
-    WaveTopK sel;
+    WaveTopKT<CAP> sel;
     sel.init(lds + wave * cap, cap, kc);
     for (int base = 0; base < nlist; base += blockDim.x) {
         const int c = base + tid;
@@ -879,8 +882,14 @@ static int ivfpq_search_run(mans_ctx* ctx, const mans_ivfpq* pq, const float* d_
             hipLaunchKernelGGL(pq_coarse_dist<kMetricCosine>, grid, dim3(256), shm, st, d_q, nq, dim, ct, nl, dists);
             break;
         }
-        hipLaunchKernelGGL(pq_probes, dim3((unsigned)nq), dim3(256), sizeof(uint64_t) * 4 * (size_t)pcap,
-                           st, (const float*)dists, nl, np, pkc, pcap, (uint32_t*)slot->aux1.p);
+        if (pcap == 256)
+            hipLaunchKernelGGL(pq_probes<256>, dim3((unsigned)nq), dim3(256),
+                               sizeof(uint64_t) * 4 * (size_t)pcap, st, (const float*)dists, nl, np,
+                               pkc, pcap, (uint32_t*)slot->aux1.p);
+        else
+            hipLaunchKernelGGL(pq_probes<0>, dim3((unsigned)nq), dim3(256),
+                               sizeof(uint64_t) * 4 * (size_t)pcap, st, (const float*)dists, nl, np,
+                               pkc, pcap, (uint32_t*)slot->aux1.p);
     }
     e = hipGetLastError();
     ctx->time_end(slot, st, "ivfpq_probe");
