@@ -742,11 +742,19 @@ __device__ __forceinline__ void lm_tile_keys(const float* qs, const float* qnorm
             acc[j] = fmaf(x.w, y.w, acc[j]);
         }
     }
+    auto put = [&](auto key_of) {
 #pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-        const int r = rs + kStep * j;
-        if (r < nvalid) tkeys[gq * S::kKeyStride + r] = lower_key(acc[j], qnorm[gq], vn[r], metric, bc);
-    }
+        for (int j = 0; j < kPer; ++j) {
+            const int r = rs + kStep * j;
+            if (r < nvalid) tkeys[gq * S::kKeyStride + r] = key_of(acc[j], qnorm[gq], vn[r]);
+        }
+    };
+    if (metric == kMetricL2)
+        put([&](float f, float qn, float v) { return lower_key_m<kMetricL2>(f, qn, v, bc); });
+    else if (metric == kMetricIP)
+        put([&](float f, float qn, float v) { return lower_key_m<kMetricIP>(f, qn, v, bc); });
+    else
+        put([&](float f, float qn, float v) { return lower_key_m<kMetricCosine>(f, qn, v, bc); });
 }
 
 // The dots of one 64-row tile on fp32 MFMA (dim <= 128): wave w takes tile
