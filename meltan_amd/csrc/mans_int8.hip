@@ -1118,8 +1118,8 @@ __global__ __launch_bounds__(kI8MergeThreads) void int8_collect_merge(
             kth = block_reduce_u64<true>(mx);
         }
         // The positions this round adds, compacted; then their rows are
-        // rescored 16 at a time (one per 16-lane group), the next group's
-        // rows in flight.
+        // rescored two per 16-lane group at a time (interleaved chains), the
+        // group's next two rows in flight.
         if (tid == 0) s_nfresh = 0;
         __syncthreads();
         for (int64_t i0 = 0; i0 < total; i0 += blockDim.x) {
@@ -1146,20 +1146,33 @@ __global__ __launch_bounds__(kI8MergeThreads) void int8_collect_merge(
                                          : f4v{0.f, 0.f, 0.f, 0.f};
             }
         };
-        auto rescore = [&](int j, const f4v (&a)[NCH]) {
+        // Rows j and j2 > j of this group (j2 may be past the last: its
+        // zero row is dotted and not written).
+        auto rescore2 = [&](int j, const f4v (&a)[NCH], int j2, const f4v (&b)[NCH]) {
             if (j >= nfresh) return;  // the whole group agrees
-            const uint32_t pos = fresh_pos[j];
-            const uint32_t id = slot_id(cand[pos]);
-            const float dot = chain_dot<NCH>(a, qv, dim4);
-            if (lr == 0) exd[pos] = host_distance(dot, qn, metric == kMetricIP ? 0.0f : norms[id], metric);
+            float d0, d1;
+            chain_dot2<NCH>(a, b, qv, dim4, d0, d1);
+            if (lr == 0) {
+                const uint32_t pos = fresh_pos[j];
+                const uint32_t id = slot_id(cand[pos]);
+                exd[pos] = host_distance(d0, qn, metric == kMetricIP ? 0.0f : norms[id], metric);
+                if (j2 < nfresh) {
+                    const uint32_t pos2 = fresh_pos[j2];
+                    const uint32_t id2 = slot_id(cand[pos2]);
+                    exd[pos2] = host_distance(d1, qn, metric == kMetricIP ? 0.0f : norms[id2], metric);
+                }
+            }
         };
-        f4v ra[NCH], rb[NCH];
+        f4v ra[NCH], rb[NCH], rc[NCH], rd[NCH];
         load_row(grp, ra);
-        for (int j0 = 0; j0 < nfresh; j0 += 2 * kGroups) {
-            load_row(j0 + kGroups + grp, rb);
-            rescore(j0 + grp, ra);
-            load_row(j0 + 2 * kGroups + grp, ra);
-            rescore(j0 + kGroups + grp, rb);
+        load_row(kGroups + grp, rb);
+        for (int j0 = 0; j0 < nfresh; j0 += 4 * kGroups) {
+            load_row(j0 + 2 * kGroups + grp, rc);
+            load_row(j0 + 3 * kGroups + grp, rd);
+            rescore2(j0 + grp, ra, j0 + kGroups + grp, rb);
+            load_row(j0 + 4 * kGroups + grp, ra);
+            load_row(j0 + 5 * kGroups + grp, rb);
+            rescore2(j0 + 2 * kGroups + grp, rc, j0 + 3 * kGroups + grp, rd);
         }
         done_cut = cut;
         __syncthreads();  // exd[] is written

@@ -243,6 +243,45 @@ __device__ __forceinline__ float chain_dot(const f4v* a, const f4v* b, int dim4)
     return __shfl(acc, row0 | last);
 }
 
+// chain_dot of two rows a0, a1 against the same b, their chains interleaved
+// (each row's operations and their order are chain_dot's): a 16-lane group
+// keeps two independent dependency chains in flight.
+template <int NCH>
+__device__ __forceinline__ void chain_dot2(const f4v* a0, const f4v* a1, const f4v* b, int dim4,
+                                           float& d0, float& d1) {
+    const int lane = __lane_id(), lr = lane & 15, row0 = lane & ~15;
+    float acc0 = 0.0f, acc1 = 0.0f;
+    int last = 0;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+#pragma unroll
+        for (int o = 0; o < 16; ++o) {
+            const int c = o + 16 * j;
+            if (c < dim4) {
+                float t0 = acc0 + a0[j].x * b[j].x;
+                float t1 = acc1 + a1[j].x * b[j].x;
+                t0 = t0 + a0[j].y * b[j].y;
+                t1 = t1 + a1[j].y * b[j].y;
+                t0 = t0 + a0[j].z * b[j].z;
+                t1 = t1 + a1[j].z * b[j].z;
+                t0 = t0 + a0[j].w * b[j].w;
+                t1 = t1 + a1[j].w * b[j].w;
+                acc0 = lr == o ? t0 : acc0;
+                acc1 = lr == o ? t1 : acc1;
+                last = o;
+                if (c + 1 < dim4) {
+                    acc0 = __int_as_float(
+                        __builtin_amdgcn_update_dpp(0, __float_as_int(acc0), 0x121, 0xF, 0xF, false));
+                    acc1 = __int_as_float(
+                        __builtin_amdgcn_update_dpp(0, __float_as_int(acc1), 0x121, 0xF, 0xF, false));
+                }
+            }
+        }
+    }
+    d0 = __shfl(acc0, row0 | last);
+    d1 = __shfl(acc1, row0 | last);
+}
+
 // Threshold merge, step 1 (the scan kernel, every block): fold the block's
 // four sorted wave lists (lds, stride cap) into its kc best (kc 32 or 64)
 // and write them and the block's head (its smallest slot) with plain stores;
